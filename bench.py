@@ -1,0 +1,235 @@
+#!/usr/bin/env python3
+"""bench.py -- one MoE layer (MoeRoutingTopK -> MoeExpertFFN -> MoeCombine) per step on one MI355X.
+
+Metric: MoE layer us; FFN TFLOPS & HBM GB/s (% peak), at the decode-size workload
+T=128, H=2048, E=16, K=2, I=8192 (fp16 I/O, fp32 accumulation) by default.
+
+A step is one pass of the layer over one batch of synthetic input resident in HBM: routing, the expert FFN
+(permute + fused gate/up/SwiGLU grouped GEMM + down grouped GEMM with the expert_out scatter) and combine, all
+through the C ABI of libmoe_mi355x.so on one stream, with caller-owned buffers allocated once.
+W warm-up steps, then K timed steps between torch.cuda.synchronize() calls; per-kernel durations come from
+HIP events that the library records around each of its launches on that same stream during the timed steps.
+
+The JSON line also carries:
+  roofline      the dominant kernel's algorithmic bytes (or flops) per launch / its average event-timed
+                duration, against MI355X's published peaks (HBM 8 TB/s, fp16 dense MFMA 2.5 PFLOP/s); `traffic`
+                is the measured HBM bytes per launch from rocprofv3 counters when profiles/traffic.json holds
+                them for this workload, else null;
+  cpu_baseline  the reference's own NaiveMoE (tests/moe_cpu_sim.cpp, built from its source into oracle/_ref),
+                single-threaded on this host, on the first tokens of the same inputs, scaled to a whole layer;
+  accuracy      this run's y on those tokens against that NaiveMoE output (the reference's thresholds).
+"""
+from __future__ import annotations
+
+import argparse
+import importlib
+import json
+import math
+import os
+import pathlib
+import platform
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+PKG = "implementing-moe-architecture-operators-on-cann-platform_amd"
+METRIC = "MoE layer µs; FFN TFLOPS & HBM GB/s (% peak) at T=128,H=2048,E=16,I=8192"
+HBM_PEAK_GBS = 8000.0
+MFMA_FP16_PEAK_TFLOPS = 2500.0
+RIDGE = MFMA_FP16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
+
+
+def progress(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def kernel_work(cfg, active_experts: int) -> dict:
+    """Algorithmic (bytes, flops) per launch of each kernel; the SwiGLU intermediate round trip through the
+    workspace is an implementation cost and is not counted."""
+    T, H, E, K, I = cfg.T, cfg.H, cfg.E, cfg.K, cfg.I
+    S = T * K
+    return {
+        "moe_routing_topk": (T * H * 2 + H * E * 2 + S * 6, 2 * T * H * E),
+        "moe_permute": (S * 4 * 2 + (E + 1) * 4, 0),
+        "moe_ffn_gateup_swiglu": (active_experts * 2 * I * H * 2 + T * H * 2, 4 * S * H * I),
+        "moe_ffn_down": (active_experts * I * H * 2 + S * H * 2, 2 * S * H * I),
+        "moe_combine": (S * H * 2 + S * 2 + T * H * 2, 2 * S * H),
+    }
+
+
+def roofline_for(name: str, bytes_, flops, avg_ms: float, traffic):
+    sec = avg_ms * 1e-3
+    intensity = flops / bytes_ if bytes_ else 0.0
+    if intensity < RIDGE:
+        achieved = bytes_ / sec / 1e9
+        return {"kernel": name, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "algorithmic_bytes": bytes_,
+                "avg_us": round(avg_ms * 1e3, 2)}
+    achieved = flops / sec / 1e12
+    return {"kernel": name, "bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_FP16_PEAK_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(achieved / MFMA_FP16_PEAK_TFLOPS, 4), "traffic": traffic,
+            "algorithmic_flops": flops, "avg_us": round(avg_ms * 1e3, 2)}
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="decode", help="workload (synth.CONFIGS); the driver uses the default")
+    ap.add_argument("--seed", type=int, default=44)
+    ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the reference CPU timing")
+    ap.add_argument("--cpu-target-gflop", type=float, default=30.0,
+                    help="size of the CPU baseline sample in GFLOP of expert FFN work")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported (this build has no multi-GPU "
+              "path; see DESIGN.md for how the layer would shard)", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    ops = importlib.import_module(f"{PKG}.ops")
+    synth = importlib.import_module(f"{PKG}.synth")
+    lib = importlib.import_module(PKG).load_library()
+    cfg = synth.CONFIGS[args.config]
+    T, H, E, K, I = cfg.T, cfg.H, cfg.E, cfg.K, cfg.I
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    progress(f"workload {cfg.name}: T={T} H={H} E={E} K={K} I={I}; generating inputs on the GPU")
+
+    x = torch.empty((T, H), dtype=torch.float16, device=dev)
+    ops.synth_normal_f16_(x, args.seed, synth.STREAM_X, 1.0)
+    wg = torch.from_numpy(synth.gen_w_gate(cfg, args.seed)).to(dev)
+    ew = torch.empty((E, 3 * I, H), dtype=torch.float16, device=dev)
+    sa, sb, period, split = synth.expert_weight_sigmas(cfg)
+    ops.synth_normal_f16_(ew, args.seed, synth.STREAM_EXPERT_WEIGHTS, sa, sb, period, split)
+    ids = torch.empty((T, K), dtype=torch.int32, device=dev)
+    w = torch.empty((T, K), dtype=torch.float16, device=dev)
+    eo = torch.empty((T, K, H), dtype=torch.float16, device=dev)
+    y = torch.empty((T, H), dtype=torch.float16, device=dev)
+    ws_bytes = ops.workspace_bytes(T, H, E, K, I)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream()
+    sp = int(stream.cuda_stream)
+    p = {k: t.data_ptr() for k, t in dict(x=x, wg=wg, ew=ew, ids=ids, w=w, eo=eo, y=y, ws=ws).items()}
+
+    def step() -> None:
+        st = lib.moe_routing_topk(p["x"], p["wg"], p["ids"], p["w"], T, H, E, K, sp)
+        st |= lib.moe_expert_ffn(p["x"], p["ids"], p["w"], p["ew"], p["eo"], p["ws"], ws_bytes, T, H, E, K, I, sp)
+        st |= lib.moe_combine(p["eo"], p["ids"], p["w"], p["y"], T, H, K, sp)
+        if st:
+            raise RuntimeError(lib.moe_last_error().decode())
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    progress(f"warm-up done ({args.warmup} steps); timing {args.steps} steps")
+
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with ops.kernel_trace() as kernels:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ev0.record(stream)
+        for _ in range(args.steps):
+            step()
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+    ms_per_step = (t1 - t0) * 1e3 / args.steps
+    gpu_ms_per_step = ev0.elapsed_time(ev1) / args.steps
+    progress(f"timed: {ms_per_step * 1e3:.1f} us/step (host clock), {gpu_ms_per_step * 1e3:.1f} us/step (events)")
+
+    ids_h = ids.cpu().numpy()
+    active = int((np.bincount(ids_h.ravel(), minlength=E) > 0).sum())
+    work = kernel_work(cfg, active)
+    per_kernel = {}
+    for name, (launches, total_ms) in kernels.items():
+        avg = total_ms / max(1, launches)
+        b, f = work.get(name, (0, 0))
+        per_kernel[name] = {"launches": launches, "avg_us": round(avg * 1e3, 2),
+                            "GB/s": round(b / (avg * 1e-3) / 1e9, 1) if b else None,
+                            "TFLOP/s": round(f / (avg * 1e-3) / 1e12, 2) if f else None}
+    ffn_names = ("moe_permute", "moe_ffn_gateup_swiglu", "moe_ffn_down")
+    ffn_ms = sum(kernels[n][1] / kernels[n][0] for n in ffn_names if n in kernels)
+    ffn_flops = 6 * T * K * H * I
+    ffn_bytes = active * 3 * I * H * 2 + T * H * 2 + T * K * H * 2
+    dominant = max(kernels, key=lambda n: kernels[n][1])
+    traffic = None
+    tfile = ROOT / "profiles" / "traffic.json"
+    if tfile.exists():
+        traffic = json.loads(tfile.read_text()).get(cfg.name, {}).get(dominant)
+    db, dflops = work[dominant]
+    roofline = roofline_for(dominant, db, dflops, kernels[dominant][1] / kernels[dominant][0], traffic)
+
+    cpu_baseline = None
+    accuracy = None
+    if not args.no_cpu_baseline:
+        import oracle
+
+        if oracle.ref_available():
+            per_token = K * 6 * H * I
+            n_s = int(max(1, min(T, round(args.cpu_target_gflop * 1e9 / per_token))))
+            progress(f"cpu baseline: reference NaiveMoE on the first {n_s} of {T} tokens (1 thread)")
+            x_s = x[:n_s].float().cpu().numpy()
+            wg_h = wg.float().cpu().numpy()
+            ew_h = ew.cpu().numpy().astype(np.float32)
+            y_ref, ref_ms = oracle.ref_moe_timed(x_s, wg_h, ew_h, K, I)
+            del ew_h
+            cpu_baseline = {"value": round(ref_ms * 1e3 * T / n_s, 1), "unit": "us", "cores": 1, "kind": "reference",
+                            "sample": f"NaiveMoE (tests/moe_cpu_sim.cpp:183-306, g++ -O2 -std=c++17) on the first "
+                                      f"{n_s} of {T} tokens, all {E} experts' weights; {ref_ms:.0f} ms scaled by "
+                                      f"{T}/{n_s} to one layer",
+                            "cpu": cpu_model(), "host_cpus": os.cpu_count()}
+            m = oracle.compare(y[:n_s].float().cpu().numpy(), y_ref)
+            accuracy = {"tokens": n_s, "max_abs": m["max_abs"], "mean_abs": m["mean_abs"], "cos": m["cos"],
+                        "pass": bool(m["max_abs"] < 0.05 and m["mean_abs"] < 0.01 and m["cos"] > 0.99)}
+            progress(f"cpu baseline {ref_ms:.0f} ms for {n_s} tokens; accuracy {accuracy}")
+        else:
+            progress("cpu baseline skipped: oracle/_ref was not built (no reference checkout at build time)")
+
+    layer_us = ms_per_step * 1e3
+    result = {
+        "metric": METRIC,
+        "value": round(layer_us, 2),
+        "unit": "us",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (counter-based N(0,1) x; N(0,1/H) w_gate, W_gate, W_up; N(0,1/I) W_down)",
+        "config": {"workload": f"{cfg.name} MoE layer T={T},H={H},E={E},K={K},I={I}", "tokens": T,
+                   "hidden": H, "experts": E, "top_k": K, "intermediate": I, "active_experts": active},
+        "layer_us_gpu_events": round(gpu_ms_per_step * 1e3, 2),
+        "ffn_us": round(ffn_ms * 1e3, 2),
+        "ffn_tflops": round(ffn_flops / (ffn_ms * 1e-3) / 1e12, 2),
+        "ffn_hbm_gbps": round(ffn_bytes / (ffn_ms * 1e-3) / 1e9, 1),
+        "ffn_hbm_frac": round(ffn_bytes / (ffn_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "ffn_mfma_frac": round(ffn_flops / (ffn_ms * 1e-3) / 1e12 / MFMA_FP16_PEAK_TFLOPS, 4),
+        "kernels": per_kernel,
+        "roofline": roofline,
+        "cpu_baseline": cpu_baseline,
+        "accuracy": accuracy,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,68 @@
+// moe_launch.h -- internal interface between the C-ABI host layer (moe_ops.cpp) and the kernel files.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace moe {
+
+// Per-kernel HIP-event timing (moe_trace.h). A TraceScope brackets exactly one kernel launch.
+class TraceScope {
+  public:
+    TraceScope(const char* name, hipStream_t stream);
+    ~TraceScope();
+    TraceScope(const TraceScope&) = delete;
+    TraceScope& operator=(const TraceScope&) = delete;
+
+  private:
+    const char* name_;
+    hipStream_t stream_;
+    hipEvent_t start_ = nullptr;
+};
+
+// ---- routing (moe_routing.hip) ----
+int routing_expert_blocks(int E);
+int routing_tokens_per_block();
+int routing_block_threads();
+int routing_lds_bytes(int E);
+hipError_t launch_routing_topk(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H,
+                               int E, int K, hipStream_t stream);
+
+// ---- expert FFN (moe_permute.hip, moe_ffn.hip) ----
+struct FfnWorkspace {
+    int32_t* offsets;      // [E + 1] first sorted row of each expert; offsets[E] = number of valid slots
+    int32_t* sorted_slot;  // [T*K]   slot index t*K + k of each sorted row, experts ascending, slots ascending
+    uint16_t* hidden;      // [T*K, I] fp16 SwiGLU intermediate, rows in sorted order
+};
+size_t ffn_workspace_bytes(int64_t T, int64_t E, int64_t K, int64_t I);
+FfnWorkspace ffn_workspace_carve(void* base, int64_t T, int64_t E, int64_t K, int64_t I);
+
+int permute_block_threads();
+hipError_t launch_permute(const int32_t* ids, int S, int E, int H, FfnWorkspace ws, uint16_t* expert_out,
+                          hipStream_t stream);
+
+struct FfnGrid {
+    int gateup_blocks;
+    int down_blocks;
+    int block_threads;
+    int rows_per_tile;
+    int schedule;
+};
+FfnGrid ffn_grid(int T, int H, int E, int K, int I);
+hipError_t launch_ffn(const uint16_t* x, const uint16_t* expert_weights, uint16_t* expert_out, FfnWorkspace ws,
+                      int T, int H, int E, int K, int I, hipStream_t stream);
+
+// ---- combine (moe_combine.hip) ----
+int combine_block_threads();
+int combine_elems_per_thread();
+int combine_grid(int64_t T, int64_t H);
+hipError_t launch_combine(const uint16_t* expert_out, const uint16_t* weights, uint16_t* y, int T, int H, int K,
+                          hipStream_t stream);
+
+// ---- synthetic inputs / calibration (moe_synth.hip) ----
+hipError_t launch_synth_normal_f16(uint16_t* out, uint64_t n, uint64_t seed, uint64_t stream_id, double sigma_a,
+                                   double sigma_b, uint64_t period, uint64_t split, hipStream_t stream);
+hipError_t launch_copy_bytes(void* dst, const void* src, uint64_t bytes, hipStream_t stream);
+
+}  // namespace moe

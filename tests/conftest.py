@@ -1,0 +1,58 @@
+"""Shared test setup: import paths, the `gpu` marker, golden-vector loading."""
+from __future__ import annotations
+
+import importlib
+import pathlib
+import sys
+
+import numpy as np
+import pytest
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+PKG_NAME = "implementing-moe-architecture-operators-on-cann-platform_amd"
+GOLDEN_DIR = ROOT / "tests" / "golden"
+GOLDEN_CASES = ["ref_small_seed42", "synth_mid_seed43", "synth_k3_seed7", "synth_dsmini_seed5"]
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU and the built HIP library")
+
+
+def package():
+    return importlib.import_module(PKG_NAME)
+
+
+def synth_module():
+    return importlib.import_module(PKG_NAME + ".synth")
+
+
+def load_golden(name: str) -> dict:
+    """Golden case -> dict with fp16 inputs x, w_gate, expert_weights (regenerated for synth cases and checked
+    against the stored SHA-256), dims (T, H, E, K, I) and the reference outputs."""
+    if str(GOLDEN_DIR) not in sys.path:
+        sys.path.insert(0, str(GOLDEN_DIR))
+    from make_golden import input_digest
+
+    data = dict(np.load(GOLDEN_DIR / f"{name}.npz", allow_pickle=False))
+    T, H, E, K, I = (int(v) for v in data["dims"])
+    if "x" not in data:
+        synth = synth_module()
+        cfg = synth.MoeConfig(T, H, E, K, I, zipf=bool(data["zipf"]))
+        data["x"], data["w_gate"], data["expert_weights"] = synth.gen_inputs(cfg, int(data["seed"]))
+    digest = input_digest(data["x"], data["w_gate"], data["expert_weights"])
+    assert digest == str(data["digest"]), f"{name}: regenerated inputs differ from the ones the fixture was made on"
+    data.update(T=T, H=H, E=E, K=K, I=I)
+    return data
+
+
+@pytest.fixture(scope="session")
+def ops():
+    """The torch-level operator API on a real GPU; skips when no GPU is visible."""
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU visible")
+    return importlib.import_module(PKG_NAME + ".ops")

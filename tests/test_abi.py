@@ -1,0 +1,170 @@
+"""The C-ABI library on the CPU: it loads, exports every function include/*.h declares, and its host logic
+(InferShape / InferDataType / planning / argument checks) behaves like the reference's op_host layer.
+No kernel is launched here: every launch call below fails validation before reaching the GPU."""
+from __future__ import annotations
+
+import ctypes as C
+import pathlib
+import re
+
+import pytest
+
+from conftest import ROOT, package
+
+pkg = package()
+lib_mod = pkg._lib
+MOE_OK, ERR_NULL, ERR_RANK, ERR_SHAPE, ERR_ARG, ERR_WS, ERR_UNSUP = 0, 1, 2, 3, 4, 5, 6
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return lib_mod.load()
+
+
+def declared_functions() -> set[str]:
+    names = set()
+    for h in sorted((ROOT / "include").glob("*.h")):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names.update(re.findall(r"^[A-Za-z_][\w \*]*?\b(moe_\w+)\s*\(", text, flags=re.M))
+    return names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    names = declared_functions()
+    assert len(names) >= 20
+    for n in sorted(names):
+        assert hasattr(lib, n), f"{n} declared in include/ but not exported"
+    assert names == set(lib_mod.SIGNATURES), "ctypes binding and headers disagree"
+
+
+def test_status_strings_and_version(lib):
+    for code, name in lib_mod.STATUS_NAMES.items():
+        assert lib.moe_status_string(code).decode() == name
+    assert b"gfx950" in lib.moe_version()
+
+
+def _routing_infer(lib, xd, wd, k):
+    ids, w = lib_mod.dims([0, 0]), lib_mod.dims([0, 0])
+    st = lib.moe_routing_topk_infer_shape(lib_mod.dims(xd), len(xd), lib_mod.dims(wd), len(wd), k, ids, w)
+    return st, tuple(ids), tuple(w)
+
+
+def test_routing_infer_shape(lib):
+    assert _routing_infer(lib, [128, 2048], [2048, 16], 2) == (MOE_OK, (128, 2), (128, 2))
+    assert _routing_infer(lib, [7, 64], [64, 4], 0) == (MOE_OK, (7, 2), (7, 2))  # attr default topK=2
+    assert _routing_infer(lib, [7, 64], [64, 8], 6)[0] == MOE_OK
+    assert _routing_infer(lib, [7, 64, 1], [64, 4], 2)[0] == ERR_RANK
+    assert _routing_infer(lib, [7, 64], [32, 4], 2)[0] == ERR_SHAPE
+    assert b"hiddenSize mismatch" in lib.moe_last_error()
+    assert _routing_infer(lib, [7, 64], [64, 4], 5)[0] == ERR_ARG
+    a, b = C.c_int32(), C.c_int32()
+    assert lib.moe_routing_topk_infer_dtype(C.byref(a), C.byref(b)) == MOE_OK
+    assert (a.value, b.value) == (lib_mod.DT_INT32, lib_mod.DT_FLOAT16)
+
+
+def _ffn_infer(lib, xd, idd, ewd, attr=0):
+    out, inter = lib_mod.dims([0, 0, 0]), C.c_int64()
+    st = lib.moe_expert_ffn_infer_shape(lib_mod.dims(xd), len(xd), lib_mod.dims(idd), len(idd), lib_mod.dims(ewd),
+                                        len(ewd), attr, out, C.byref(inter))
+    return st, tuple(out), inter.value
+
+
+def test_expert_ffn_infer_shape(lib):
+    assert _ffn_infer(lib, [128, 2048], [128, 2], [16, 3 * 8192, 2048]) == (MOE_OK, (128, 2, 2048), 8192)
+    assert _ffn_infer(lib, [128, 2048], [128, 2], [16, 3 * 8192, 2048], 8192)[0] == MOE_OK
+    assert _ffn_infer(lib, [128, 2048], [128, 2], [16, 3 * 8192, 2048], 4096)[0] == ERR_SHAPE
+    assert _ffn_infer(lib, [128, 2048], [128, 2], [16, 3 * 8192 + 1, 2048])[0] == ERR_SHAPE
+    assert _ffn_infer(lib, [128, 2048], [128, 2], [16, 3 * 8192])[0] == ERR_RANK
+    assert _ffn_infer(lib, [128, 2048], [128], [16, 3 * 8192, 2048])[0] == ERR_RANK
+    assert _ffn_infer(lib, [128, 2048], [64, 2], [16, 3 * 8192, 2048])[0] == ERR_SHAPE
+    assert _ffn_infer(lib, [128, 1024], [128, 2], [16, 3 * 8192, 2048])[0] == ERR_SHAPE
+    dt = C.c_int32()
+    assert lib.moe_expert_ffn_infer_dtype(C.byref(dt)) == MOE_OK and dt.value == lib_mod.DT_FLOAT16
+
+
+def test_combine_infer_shape(lib):
+    y = lib_mod.dims([0, 0])
+    assert lib.moe_combine_infer_shape(lib_mod.dims([128, 2, 2048]), 3, lib_mod.dims([128, 2]), 2, y) == MOE_OK
+    assert tuple(y) == (128, 2048)
+    assert lib.moe_combine_infer_shape(lib_mod.dims([128, 2, 2048]), 3, None, 0, y) == MOE_OK
+    assert lib.moe_combine_infer_shape(lib_mod.dims([128, 2048]), 2, None, 0, y) == ERR_RANK
+    assert lib.moe_combine_infer_shape(lib_mod.dims([128, 2, 2048]), 3, lib_mod.dims([128, 3]), 2, y) == ERR_SHAPE
+    assert lib.moe_combine_infer_shape(lib_mod.dims([128, 2, 2048]), 3, lib_mod.dims([128, 2, 1]), 3, y) == ERR_RANK
+
+
+def test_plans(lib):
+    rp = lib_mod.RoutingPlan()
+    assert lib.moe_routing_topk_plan(128, 2048, 16, 2, C.byref(rp)) == MOE_OK
+    assert (rp.grid, rp.block, rp.tokens_per_block, rp.workspace_bytes) == (8, 256, 16, 0)
+    assert lib.moe_routing_topk_plan(128, 2040, 16, 2, C.byref(rp)) == ERR_UNSUP
+    assert lib.moe_routing_topk_plan(128, 2048, 300, 2, C.byref(rp)) == ERR_UNSUP
+    fp = lib_mod.FfnPlan()
+    assert lib.moe_expert_ffn_plan(128, 2048, 16, 2, 8192, C.byref(fp)) == MOE_OK
+    ws = lib.moe_expert_ffn_workspace_bytes(128, 2048, 16, 2, 8192)
+    assert fp.workspace_bytes == ws
+    # offsets + sorted slots + the fp16 [T*K, I] intermediate, each 256-byte aligned
+    assert ws == 256 + 1024 + 128 * 2 * 8192 * 2
+    assert fp.permute_grid == 16 and fp.gateup_grid > 0 and fp.down_grid > 0
+    assert lib.moe_expert_ffn_workspace_bytes(128, 2048, 16, 2, 8200) == 0  # I % 32 != 0
+    assert lib.moe_expert_ffn_plan(16384, 2048, 64, 6, 1408, C.byref(fp)) == MOE_OK
+    cp = lib_mod.CombinePlan()
+    assert lib.moe_combine_plan_for(128, 2048, 2, C.byref(cp)) == MOE_OK
+    assert cp.grid * cp.block * cp.elems_per_thread >= 128 * 2048 and cp.workspace_bytes == 0
+
+
+FAKE = 1 << 20  # non-null, 16-byte aligned, never dereferenced: every call below fails validation first
+
+
+def test_launch_argument_errors_return_before_launch(lib):
+    assert lib.moe_routing_topk(None, None, None, None, 4, 64, 4, 2, None) == ERR_NULL
+    assert lib.moe_routing_topk(FAKE, FAKE, FAKE, FAKE, 4, 64, 4, 5, None) == ERR_ARG
+    assert lib.moe_routing_topk(FAKE, FAKE, FAKE, FAKE, 4, 60, 4, 2, None) == ERR_UNSUP
+    assert lib.moe_routing_topk(FAKE + 2, FAKE, FAKE, FAKE, 4, 64, 4, 2, None) == ERR_UNSUP  # misaligned x
+    assert lib.moe_routing_topk(None, None, None, None, 0, 64, 4, 2, None) == MOE_OK  # T = 0: no-op
+    need = lib.moe_expert_ffn_workspace_bytes(4, 64, 4, 2, 256)
+    args = (4, 64, 4, 2, 256, None)
+    assert lib.moe_expert_ffn(FAKE, FAKE, FAKE, FAKE, FAKE, None, need, *args) == ERR_WS
+    assert lib.moe_expert_ffn(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, need - 1, *args) == ERR_WS
+    assert b"need" in lib.moe_last_error()
+    assert lib.moe_expert_ffn(None, FAKE, FAKE, FAKE, FAKE, FAKE, need, *args) == ERR_NULL
+    assert lib.moe_expert_ffn(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, need, 4, 64, 4, 5, 256, None) == ERR_ARG
+    assert lib.moe_expert_ffn(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, need, 4, 64, 4, 2, 0, None) == ERR_ARG
+    assert lib.moe_combine(None, None, None, None, 4, 64, 2, None) == ERR_NULL
+    assert lib.moe_combine(FAKE, None, FAKE, FAKE, 4, 60, 2, None) == ERR_UNSUP
+    assert lib.moe_combine(FAKE, None, FAKE, FAKE, 4, 64, 0, None) == ERR_ARG
+    assert lib.moe_synth_normal_f16(None, 10, 0, 0, 1.0, 1.0, 1, 1, None) == ERR_NULL
+    assert lib.moe_copy_bytes(FAKE, FAKE, 17, None) == ERR_ARG
+
+
+def test_last_error_is_cleared_on_success(lib):
+    assert _routing_infer(lib, [7, 64], [32, 4], 2)[0] == ERR_SHAPE
+    assert lib.moe_last_error() != b""
+    assert _routing_infer(lib, [7, 64], [64, 4], 2)[0] == MOE_OK
+    assert lib.moe_last_error() == b""
+
+
+def test_trace_api_without_launches(lib):
+    assert lib.moe_trace_enable(1) == MOE_OK
+    assert lib.moe_trace_collect() == 0
+    assert lib.moe_trace_get(0, None, None, None) == ERR_ARG
+    assert lib.moe_trace_enable(0) == MOE_OK
+
+
+def test_python_mirror_validates_before_launch():
+    torch = pytest.importorskip("torch")
+    ops = pkg.ops
+    with pytest.raises(lib_mod.MoeError):
+        ops.MoeRoutingTopK(torch.zeros(4, 64, dtype=torch.float16), torch.zeros(64, 4, dtype=torch.float16))  # CPU
+    assert ops.infer_routing((9, 64), (64, 8), 3)[0] == ((9, 3), torch.int32)
+    assert ops.infer_expert_ffn((9, 64), (9, 3), (8, 96, 64))[:2] == ((9, 3, 64), torch.float16)
+    assert ops.infer_combine((9, 3, 64))[0] == (9, 64)
+    with pytest.raises(lib_mod.MoeError) as err:
+        ops.infer_expert_ffn((9, 64), (9, 3), (8, 96, 64), intermediateSize=64)
+    assert err.value.status == ERR_SHAPE
+
+
+def test_package_fails_loudly_without_library(tmp_path, monkeypatch):
+    monkeypatch.setattr(lib_mod, "LIB_PATH", pathlib.Path(tmp_path) / "missing.so")
+    monkeypatch.setattr(lib_mod, "_lib", None)
+    with pytest.raises(RuntimeError, match="no\\s+CPU fallback"):
+        lib_mod.load()

@@ -1,0 +1,290 @@
+"""Parity of the HIP path (libmoe_mi355x.so through its C ABI) with the oracle and the reference's vectors.
+
+Bars (thresholds from tests/test_moe.cpp:486-490):
+  expert_ids  bit-exact, except tokens whose K-th and (K+1)-th probabilities, or two adjacent ranks inside
+              the top K, differ by less than 1e-3 (reported, not failed);
+  weights, expert_out, y   max abs < 0.05, mean abs < 0.01, cosine > 0.99, plus the tighter fp16 bounds below;
+  combine     bit-exact against the oracle's fp32 combine of the same fp16 inputs, rounded to fp16;
+  permute     bit-exact against a stable sort of the slots by expert.
+Tolerance sources: fp16 rounding of weights, the SwiGLU intermediate, expert_out and y (relative 2^-11
+each) and fp32 summation order (MFMA accumulation vs the oracle's sequential sums, ~sqrt(n) * 2^-24 relative).
+At the BASELINE sizes the oracle runs on a sample of tokens; everything else is checked in full.
+"""
+from __future__ import annotations
+
+import math
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import GOLDEN_CASES, load_golden, synth_module
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+synth = synth_module()
+
+NS = dict(max_abs=0.05, mean_abs=0.01, cos=0.99)  # north_star thresholds
+TIE_GAP = 1e-3
+
+
+def log(msg: str) -> None:
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def dev(a: np.ndarray) -> "torch.Tensor":
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t: "torch.Tensor") -> np.ndarray:
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def f32(a) -> np.ndarray:
+    return np.asarray(a, dtype=np.float32)
+
+
+def within(metrics: dict, max_abs: float = NS["max_abs"], mean_abs: float = NS["mean_abs"], cos: float = NS["cos"]):
+    assert metrics["max_abs"] < max_abs, metrics
+    assert metrics["mean_abs"] < mean_abs, metrics
+    assert metrics["cos"] > cos, metrics
+
+
+def check_routing(ids_g: np.ndarray, w_g: np.ndarray, x16, wg16, K: int, tag: str):
+    ids_o, w_o, probs, _ = oracle.routing(f32(x16), f32(wg16), K)
+    boundary, inner = oracle.topk_gaps(probs, K)
+    near = (boundary < TIE_GAP) | (inner < TIE_GAP)
+    differ = (ids_g != ids_o).any(axis=1)
+    log(f"[{tag}] routing: {len(ids_g)} tokens, {int(near.sum())} near-tie (gap < {TIE_GAP}), "
+        f"{int(differ.sum())} with different ids, all of them near-tie: {bool(not (differ & ~near).any())}")
+    assert not (differ & ~near).any(), np.nonzero(differ & ~near)[0][:10]
+    w_g = f32(w_g)
+    ok = ~near
+    if ok.any():
+        # fp16 weights in [0, 1]: one fp16 ulp is <= 2^-11; logits summed in another order move p by ~1e-7
+        assert np.max(np.abs(w_g[ok] - w_o[ok])) <= 2.0**-10
+    within(oracle.compare(w_g, w_o))
+    np.testing.assert_allclose(w_g.astype(np.float64).sum(axis=1), 1.0, atol=K * 2.0**-11)
+    return ids_o, w_o
+
+
+def check_permute(ws: np.ndarray, ids: np.ndarray, E: int):
+    S = ids.size
+    off_bytes = ((4 * (E + 1) + 255) // 256) * 256
+    offsets = ws[: 4 * (E + 1)].view(np.int32)
+    sorted_slot = ws[off_bytes: off_bytes + 4 * S].view(np.int32)
+    flat = ids.ravel()
+    valid = (flat >= 0) & (flat < E)
+    expect_sorted = np.nonzero(valid)[0][np.argsort(flat[valid], kind="stable")]
+    expect_off = np.concatenate([[0], np.cumsum(np.bincount(flat[valid], minlength=E))]).astype(np.int32)
+    assert np.array_equal(offsets, expect_off)
+    assert np.array_equal(sorted_slot[: expect_sorted.size], expect_sorted.astype(np.int32))
+
+
+def run_ffn(ops, x_d, ids_d, w_d, ew_d, I):
+    T, H = x_d.shape
+    E, K = ew_d.shape[0], ids_d.shape[1]
+    ws = torch.empty(ops.workspace_bytes(T, H, E, K, I), dtype=torch.uint8, device="cuda")
+    eo = ops.MoeExpertFFN(x_d, ids_d, w_d, ew_d, 0, ws)
+    return eo, ws
+
+
+# ------------------------------------------------------------------------------------------------------------
+# golden vectors (reference outputs) and stage-wise parity at the small shapes
+# ------------------------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("case", GOLDEN_CASES)
+def test_layer_matches_reference_golden(ops, case):
+    log(f"[golden {case}] start")
+    g = load_golden(case)
+    K, I, E = g["K"], g["I"], g["E"]
+    x_d, wg_d, ew_d = dev(g["x"]), dev(g["w_gate"]), dev(g["expert_weights"])
+
+    ids_d, w_d = ops.MoeRoutingTopK(x_d, wg_d, K)
+    ids, w = host(ids_d), host(w_d)
+    check_routing(ids, w, g["x"], g["w_gate"], K, case)
+    near_free = np.array_equal(ids, g["expert_ids"])
+
+    eo_d, ws = run_ffn(ops, x_d, ids_d, w_d, ew_d, I)
+    eo = f32(host(eo_d))
+    check_permute(host(ws), ids, E)
+    eo_o = oracle.expert_ffn(f32(g["x"]), ids, f32(g["expert_weights"]), I)
+    m_eo = oracle.compare(eo, eo_o)
+    log(f"[golden {case}] expert_out vs oracle: {m_eo}")
+    within(m_eo, max_abs=1e-2, mean_abs=1e-3, cos=0.9999)
+    if near_free:
+        within(oracle.compare(eo, g["expert_out_tiled"]), max_abs=1e-2, mean_abs=1e-3, cos=0.9999)
+
+    y_d = ops.MoeCombine(eo_d, ids_d, w_d, K)
+    y = host(y_d)
+    y_o = oracle.combine(eo, f32(w)).astype(np.float16)
+    assert np.array_equal(y.view(np.uint16), y_o.view(np.uint16)), "combine not bit-exact"
+    m_y = oracle.compare(f32(y), g["y_naive"])
+    log(f"[golden {case}] y vs reference NaiveMoE: {m_y}")
+    within(m_y)
+    within(m_y, max_abs=1e-2, mean_abs=1e-3, cos=0.9999)
+
+
+def test_moe_layer_chain_equals_stagewise(ops):
+    g = load_golden("synth_mid_seed43")
+    x_d, wg_d, ew_d = dev(g["x"]), dev(g["w_gate"]), dev(g["expert_weights"])
+    y, ids, w, eo = ops.moe_layer(x_d, wg_d, ew_d, g["K"])
+    ids2, w2 = ops.MoeRoutingTopK(x_d, wg_d, g["K"])
+    eo2, _ = run_ffn(ops, x_d, ids2, w2, ew_d, g["I"])
+    y2 = ops.MoeCombine(eo2, ids2, w2)
+    for a, b in ((y, y2), (ids, ids2), (w, w2), (eo, eo2)):
+        assert torch.equal(a, b)  # deterministic: no atomics anywhere on the path
+
+
+def test_combine_bit_exact_random(ops):
+    rng = np.random.default_rng(0)
+    for T, H, K in ((1, 8, 1), (37, 64, 2), (300, 2048, 6), (5, 4096, 32)):
+        eo = (rng.standard_normal((T, K, H)) * 2).astype(np.float16)
+        w = rng.random((T, K)).astype(np.float16)
+        y = host(ops.MoeCombine(dev(eo), None, dev(w), K))
+        y_o = oracle.combine(f32(eo), f32(w)).astype(np.float16)
+        assert np.array_equal(y.view(np.uint16), y_o.view(np.uint16)), (T, H, K)
+
+
+def test_combine_k1_is_copy_and_equal_weights_mean(ops):
+    rng = np.random.default_rng(1)
+    eo = rng.standard_normal((9, 1, 128)).astype(np.float16)
+    y = host(ops.MoeCombine(dev(eo), None, dev(np.ones((9, 1), np.float16))))
+    assert np.array_equal(y.view(np.uint16), eo[:, 0].view(np.uint16))
+
+
+@pytest.mark.parametrize("T,H,E,K", [(37, 64, 4, 2), (16, 96, 8, 8), (200, 256, 64, 6), (5, 32, 256, 32),
+                                     (1, 2048, 16, 2), (33, 128, 1, 1), (1000, 512, 130, 4)])
+def test_routing_shapes(ops, T, H, E, K):
+    rng = np.random.default_rng(T * 1000 + E)
+    x = rng.standard_normal((T, H)).astype(np.float16)
+    wg = (rng.standard_normal((H, E)) / math.sqrt(H)).astype(np.float16)
+    ids_d, w_d = ops.MoeRoutingTopK(dev(x), dev(wg), K)
+    check_routing(host(ids_d), host(w_d), x, wg, K, f"routing T{T} H{H} E{E} K{K}")
+
+
+def test_routing_exact_ties_lowest_index_first(ops):
+    # all-equal logits: the same SET as the reference (lowest K indices), listed in ascending order
+    T, H, E, K = 4, 64, 8, 5
+    ids, w = ops.MoeRoutingTopK(dev(np.zeros((T, H), np.float16)), dev(np.zeros((H, E), np.float16)), K)
+    assert (host(ids) == np.arange(K)).all()
+    assert (f32(host(w)) == np.float32(np.float16(0.2))).all()
+
+
+def test_ffn_edge_routings(ops):
+    # one expert takes every row (multi-pass over row tiles), others none; K=1; ids out of range -> zero rows
+    rng = np.random.default_rng(2)
+    T, H, E, K, I = 200, 64, 3, 2, 96
+    x = rng.standard_normal((T, H)).astype(np.float16)
+    ew = np.concatenate([rng.standard_normal((E, 2 * I, H)) / math.sqrt(H),
+                         rng.standard_normal((E, I, H)) / math.sqrt(I)], axis=1).astype(np.float16)
+    ids = np.zeros((T, K), np.int32)
+    ids[:, 1] = 2
+    ids[5, 0] = -1
+    ids[7, 1] = E
+    w = np.full((T, K), 0.5, np.float16)
+    eo_d, ws = run_ffn(ops, dev(x), dev(ids), dev(w), dev(ew), I)
+    eo = f32(host(eo_d))
+    check_permute(host(ws), ids, E)
+    assert not eo[5, 0].any() and not eo[7, 1].any()
+    ids_ok = ids.copy()
+    ids_ok[5, 0] = 0
+    ids_ok[7, 1] = 0
+    eo_o = oracle.expert_ffn(f32(x), ids_ok, f32(ew), I)
+    mask = np.ones((T, K), bool)
+    mask[5, 0] = mask[7, 1] = False
+    within(oracle.compare(eo[mask], eo_o[mask]), max_abs=1e-2, mean_abs=1e-3, cos=0.9999)
+
+
+def test_ffn_rejects_bad_workspace(ops):
+    x = dev(np.zeros((4, 64), np.float16))
+    ids = dev(np.zeros((4, 2), np.int32))
+    w = dev(np.zeros((4, 2), np.float16))
+    ew = dev(np.zeros((4, 3 * 32, 64), np.float16))
+    small = torch.empty(16, dtype=torch.uint8, device="cuda")
+    with pytest.raises(ops.MoeError) as err:
+        ops.MoeExpertFFN(x, ids, w, ew, 0, small)
+    assert err.value.status == 5
+
+
+# ------------------------------------------------------------------------------------------------------------
+# the GPU generator equals the numpy spec
+# ------------------------------------------------------------------------------------------------------------
+
+def test_gpu_synth_matches_numpy(ops):
+    n = 1 << 20
+    sa, sb, period, split = 0.02, 0.011, 3 * 96 * 64, 2 * 96 * 64
+    t = torch.empty(n, dtype=torch.float16, device="cuda")
+    ops.synth_normal_f16_(t, 44, 3, sa, sb, period, split)
+    ref = synth.normal_f16(44, 3, n, sa, sb, period, split)
+    assert np.array_equal(host(t).view(np.uint16), ref.view(np.uint16))
+    t2 = torch.empty(4097, dtype=torch.float16, device="cuda")
+    ops.synth_normal_f16_(t2, 5, 1, 1.0)
+    assert np.array_equal(host(t2).view(np.uint16), synth.normal_f16(5, 1, 4097, 1.0).view(np.uint16))
+
+
+# ------------------------------------------------------------------------------------------------------------
+# BASELINE sizes: inputs generated on the GPU, oracle on a token sample
+# ------------------------------------------------------------------------------------------------------------
+
+def gpu_inputs(ops, cfg, seed: int):
+    """x and expert_weights from the GPU generator, w_gate from numpy (it carries the Zipf scaling)."""
+    x = torch.empty((cfg.T, cfg.H), dtype=torch.float16, device="cuda")
+    ops.synth_normal_f16_(x, seed, synth.STREAM_X, 1.0)
+    ew = torch.empty((cfg.E, 3 * cfg.I, cfg.H), dtype=torch.float16, device="cuda")
+    sa, sb, period, split = synth.expert_weight_sigmas(cfg)
+    ops.synth_normal_f16_(ew, seed, synth.STREAM_EXPERT_WEIGHTS, sa, sb, period, split)
+    wg = dev(synth.gen_w_gate(cfg, seed))
+    return x, wg, ew
+
+
+@pytest.mark.parametrize("name", ["decode", "prefill", "deepseek", "mixtral"])
+def test_baseline_config_sampled(ops, name):
+    cfg = synth.CONFIGS[name]
+    log(f"[{name}] T={cfg.T} H={cfg.H} E={cfg.E} K={cfg.K} I={cfg.I}: generating inputs on the GPU")
+    x_d, wg_d, ew_d = gpu_inputs(ops, cfg, 44)
+    # spot-check the device generator against numpy on slices of both weight blocks
+    ew_flat = ew_d.view(-1)
+    sa, sb, period, split = synth.expert_weight_sigmas(cfg)
+    for start in (0, split - 1000, period * (cfg.E - 1) + split):
+        got = host(ew_flat[start:start + 2000])
+        raw = synth.normal_f64(44, synth.STREAM_EXPERT_WEIGHTS, start, 2000)
+        sig = np.where((np.arange(start, start + 2000) % period) < split, sa, sb)
+        assert np.array_equal(got.view(np.uint16), (raw * sig).astype(np.float16).view(np.uint16))
+
+    ids_d, w_d = ops.MoeRoutingTopK(x_d, wg_d, cfg.K)
+    ids, w = host(ids_d), host(w_d)
+    x16 = host(x_d)
+    check_routing(ids, w, x16, host(wg_d), cfg.K, name)
+    counts = np.bincount(ids.ravel(), minlength=cfg.E)
+    log(f"[{name}] rows per expert: min {counts.min()} max {counts.max()}")
+
+    eo_d, ws = run_ffn(ops, x_d, ids_d, w_d, ew_d, cfg.I)
+    check_permute(host(ws[: 4 * (cfg.E + 1) + 256 + 4 * cfg.slots]), ids, cfg.E)
+    y_d = ops.MoeCombine(eo_d, ids_d, w_d, cfg.K)
+    torch.cuda.synchronize()
+
+    sample = np.unique(np.linspace(0, cfg.T - 1, 6).astype(int))
+    used = np.unique(ids[sample])
+    ew_host = np.zeros((cfg.E, 3 * cfg.I, cfg.H), np.float32)
+    for e in used:
+        ew_host[e] = f32(host(ew_d[int(e)]))
+    eo_o = oracle.expert_ffn(f32(x16[sample]), ids[sample], ew_host, cfg.I)
+    eo_s = f32(host(eo_d))[sample]
+    m_eo = oracle.compare(eo_s, eo_o)
+    log(f"[{name}] expert_out on tokens {sample.tolist()}: {m_eo}")
+    within(m_eo, max_abs=1e-2, mean_abs=1e-3, cos=0.9999)
+    y_s = f32(host(y_d))[sample]
+    y_o = oracle.combine(eo_o, f32(w[sample]))
+    m_y = oracle.compare(y_s, y_o)
+    log(f"[{name}] y on sampled tokens: {m_y}")
+    within(m_y)
+    within(m_y, max_abs=1e-2, mean_abs=1e-3, cos=0.9999)
+    # size-independent check over all tokens: y equals the combine of the full expert_out (bit-exact)
+    y_all = host(y_d)
+    y_chk = oracle.combine(f32(host(eo_d)), f32(w)).astype(np.float16)
+    assert np.array_equal(y_all.view(np.uint16), y_chk.view(np.uint16))
+    assert np.isfinite(f32(y_all)).all()
