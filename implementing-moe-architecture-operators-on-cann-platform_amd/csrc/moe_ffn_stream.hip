@@ -1,0 +1,354 @@
+// moe_ffn_stream.hip -- weight-streaming schedule of the MoeExpertFFN grouped GEMMs (few rows per expert).
+//
+// Reference: op_kernel/moe_expert_ffn.cpp (ComputeSwiGLU :265-333, ComputeDownProj :339-394, scatter :250-257);
+// oracle: tests/moe_cpu_sim.cpp:245-296 (W_gate, W_up [I, H]; W_down [H, I]).
+//
+// With few rows per expert (decode: T = 128, K = 2, E = 16 -> ~16 rows) each weight byte serves only those
+// rows, so the GEMMs are bound by streaming E*3*I*H*2 bytes from HBM once. What the MI355X measurements behind
+// this design showed (pure load kernels at the real [E, 3I, H] layout):
+//   * a wave streaming weight rows with D k-steps of loads in flight sustains ~6 TB/s, even at 2 waves/SIMD;
+//   * activation loads issued through the same vector-memory queue cost 10-40%: loads retire in order and the
+//     L2-served traffic competes with the HBM stream -> activations are staged in LDS once per workgroup;
+//   * all waves walking the rows in the same k order hit the same address-mod-4KB at the same time (rows are
+//     4 KB / 16 KB apart): starting each wave at a different k (rotation) is worth ~10%;
+//   * register spills in the loop are fatal: scratch reloads also wait on the vector-memory counter and drain
+//     the weight ring -> 8 waves per workgroup, no spills (checked with -Rpass-analysis=kernel-resource-usage).
+//
+// Workgroup = 8 waves on one expert e and one K-range [k0, k0 + kc):
+//   1. the workgroup copies the K-range of the expert's activation rows (up to 32 per pass; x rows gathered
+//      through the sorted slot order for gate/up, SwiGLU rows for down) into LDS, then one barrier;
+//   2. each wave streams two 16-row weight tiles (gate/up: W_gate and W_up rows n0..n0+15; down: W_down rows
+//      n0..n0+31) through a register ring of D k-steps, starting at its own rotated step, with activation
+//      fragments read from LDS (ds_read_b128) and v_mfma_f32_16x16x32_f16 (fp32 accumulation);
+//   3. epilogue in registers: gate/up -> hidden = silu(gate) * up (fp32) -> fp16 workspace row;
+//      down with one K-range -> expert_out[slot] fp16 (the scatter back to [T, K, H] order);
+//      down with several K-ranges -> fp32 partial sums, added in a fixed order by down_reduce_kernel (no atomics,
+//      deterministic).
+// An expert with more than 32 rows takes several passes, each re-streaming the weights: this schedule is
+// chosen only when the average number of rows per expert is small.
+// LDS: row r of the staged K-range at r * (kc + 8) halfs (16 B of padding per row puts the 16 rows read by one
+// ds_read_b128 in different banks).
+
+#include "moe_device.h"
+#include "moe_launch.h"
+
+namespace moe {
+
+namespace {
+
+constexpr int kWaves = 8;                 // streaming waves per workgroup
+constexpr int kThreads = kWaves * kWave;  // 512
+constexpr int kMaxRows = 32;              // activation rows per pass (two 16-row MFMA tiles)
+constexpr int kLdsMax = 160 * 1024;       // gfx950 LDS per workgroup
+
+enum Epilogue { kSwiGLU = 0, kScatter = 1, kPartial = 2 };
+
+struct StreamArgs {
+    const uint16_t* act;          // activation rows: x [T, H] (gate/up) or hidden [T*K, I] (down)
+    const int32_t* sorted_slot;   // [T*K]
+    const int32_t* offsets;       // [E+1]
+    const uint16_t* w;            // expert_weights [E, 3I, H]
+    uint16_t* out;                // hidden (kSwiGLU) or expert_out (kScatter)
+    float* partial;               // [nsplit][T*K][H] fp32 (kPartial)
+    int K, H, I;
+    int kdim;                     // reduction extent: H (gate/up) or I (down)
+    int ndim;                     // output columns: I (gate/up) or H (down)
+    int kc;                       // K-range per workgroup (kdim % kc == 0, (kc / 32) % D == 0)
+    int rows_cap;                 // activation rows per pass: 32, or 16 when 32 rows of kc do not fit LDS
+    int nsplit;                   // kdim / kc
+    int total_rows;               // T*K (partial buffer stride)
+    size_t w_off;                 // first weight matrix inside an expert block: 0 (gate) or 2*I*H (down)
+    size_t w1_off;                // second weight tile relative to the first: I*H (up) or 16*I (next 16 rows)
+    int gather;                   // activation row r is x[sorted_slot[r] / K] (gate/up) or hidden[r] (down)
+};
+
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+__device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)); }
+
+// D k-steps on ring slots 0..D-1: activation fragments from LDS at physical step `ph`, then (REFILL) reload
+// each slot with physical step `pn` + i.
+template <int MT, int D, bool REFILL>
+__device__ __forceinline__ void ring_batch(const uint16_t* lds, int stride, int ph, int pn, int row, int kg,
+                                           const uint16_t* w0, const uint16_t* w1, f16x8 (&r0)[D], f16x8 (&r1)[D],
+                                           f32x4 (&acc0)[MT], f32x4 (&acc1)[MT]) {
+#pragma unroll
+    for (int i = 0; i < D; ++i) {
+        f16x8 a[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+            a[mt] = *reinterpret_cast<const f16x8*>(lds + (mt * 16 + row) * stride + (ph + i) * 32 + kg * 8);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            acc0[mt] = mfma16x16x32(a[mt], r0[i], acc0[mt]);
+            acc1[mt] = mfma16x16x32(a[mt], r1[i], acc1[mt]);
+        }
+        if (REFILL) {
+            r0[i] = load_f16x8(w0 + (pn + i) * 32);
+            r1[i] = load_f16x8(w1 + (pn + i) * 32);
+        }
+    }
+}
+
+// Whole K-range of one pass for one wave; the ring was primed by the caller at step `rot`.
+template <int MT, int D, int EPI>
+__device__ __forceinline__ void ring_pass(const StreamArgs& p, const uint16_t* lds, const uint16_t* w0,
+                                          const uint16_t* w1, f16x8 (&r0)[D], f16x8 (&r1)[D], int rot, int off,
+                                          int ne, int mc, int n0, int split, int lane) {
+    const int row = lane & 15, kg = lane >> 4;
+    const int nsteps = p.kc / 32;
+    const int stride = p.kc + 8;
+    f32x4 acc0[MT], acc1[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        acc0[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        acc1[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    for (int s0 = 0; s0 < nsteps; s0 += D) {
+        const int ph = s0 + rot < nsteps ? s0 + rot : s0 + rot - nsteps;
+        const int pn = s0 + D + rot < nsteps ? s0 + D + rot : s0 + D + rot - nsteps;
+        if (s0 + D < nsteps)
+            ring_batch<MT, D, true>(lds, stride, ph, pn, row, kg, w0, w1, r0, r1, acc0, acc1);
+        else
+            ring_batch<MT, D, false>(lds, stride, ph, pn, row, kg, w0, w1, r0, r1, acc0, acc1);
+    }
+    // D[m][n]: m = 4*kg + j (activation row of tile mt), n = row (weight row of the tile)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int m = mc + mt * 16 + kg * 4 + j;
+            if (m >= ne) continue;
+            if (EPI == kSwiGLU) {
+                const float hv = silu_f32(acc0[mt][j]) * acc1[mt][j];
+                p.out[static_cast<size_t>(off + m) * p.ndim + n0 + row] = f32_to_f16_bits(hv);
+            } else if (EPI == kScatter) {
+                const size_t o = static_cast<size_t>(p.sorted_slot[off + m]) * p.ndim + n0 + row;
+                p.out[o] = f32_to_f16_bits(acc0[mt][j]);
+                p.out[o + 16] = f32_to_f16_bits(acc1[mt][j]);
+            } else {
+                float* dst = p.partial + (static_cast<size_t>(split) * p.total_rows + off + m) * p.ndim + n0 + row;
+                dst[0] = acc0[mt][j];
+                dst[16] = acc1[mt][j];
+            }
+        }
+}
+
+// Grid: E * groups * nsplit workgroups; workgroup -> (expert, column group, K-range).
+template <int D, int EPI>
+__global__ __launch_bounds__(kThreads) void ffn_stream_kernel(StreamArgs p) {
+    extern __shared__ __align__(16) uint16_t lds[];
+    const int wave = static_cast<int>(threadIdx.x) / kWave;
+    const int lane = lane_id();
+    const int cols_per_wave = EPI == kSwiGLU ? 16 : 32;  // gate/up: 16 rows of each matrix; down: 32 rows
+    const int groups = (p.ndim + kWaves * cols_per_wave - 1) / (kWaves * cols_per_wave);
+    const int b = static_cast<int>(blockIdx.x);
+    const int split = b % p.nsplit;
+    const int e = b / p.nsplit / groups;
+    const int n0 = ((b / p.nsplit) % groups * kWaves + wave) * cols_per_wave;
+    const int off = p.offsets[e];
+    const int ne = p.offsets[e + 1] - off;
+    if (ne <= 0) return;  // uniform over the workgroup
+    const bool active = n0 < p.ndim;
+    const int row = lane & 15, kg = lane >> 4;
+    const int nsteps = p.kc / 32;
+    const int k0 = split * p.kc;
+    const size_t ebase = static_cast<size_t>(e) * 3 * static_cast<size_t>(p.I) * p.H;
+    const uint16_t* w0 = p.w + ebase + p.w_off + static_cast<size_t>(active ? n0 + row : row) * p.kdim + k0 + kg * 8;
+    const uint16_t* w1 = w0 + p.w1_off;
+    const int rot = ((b * kWaves + wave) * 7 * D) % nsteps;  // a multiple of D: batches never wrap
+    const int gpr = p.kc / 8;
+    const int stride = p.kc + 8;
+
+    for (int mc = 0; mc < ne; mc += p.rows_cap) {
+        const int rows = min(p.rows_cap, ne - mc);
+        f16x8 r0[D], r1[D];
+        if (active) {
+#pragma unroll
+            for (int i = 0; i < D; ++i) {
+                r0[i] = load_f16x8(w0 + (rot + i) * 32);
+                r1[i] = load_f16x8(w1 + (rot + i) * 32);
+            }
+        }
+        if (mc > 0) lds_barrier();  // every wave is done with the previous pass's rows
+        const int total = rows * gpr;
+        for (int q0 = 0; q0 < total; q0 += 4 * kThreads) {
+            u32x4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int q = q0 + u * kThreads + static_cast<int>(threadIdx.x);
+                if (q < total) {
+                    const int r = q / gpr;
+                    const size_t src_row = p.gather ? static_cast<size_t>(p.sorted_slot[off + mc + r] / p.K)
+                                                    : static_cast<size_t>(off + mc + r);
+                    v[u] = *reinterpret_cast<const u32x4*>(p.act + src_row * p.kdim + k0 + (q % gpr) * 8);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int q = q0 + u * kThreads + static_cast<int>(threadIdx.x);
+                if (q < total) *reinterpret_cast<u32x4*>(lds + (q / gpr) * stride + (q % gpr) * 8) = v[u];
+            }
+        }
+        lds_barrier();
+        if (!active) continue;
+        if (rows > 16)
+            ring_pass<2, D, EPI>(p, lds, w0, w1, r0, r1, rot, off, ne, mc, n0, split, lane);
+        else
+            ring_pass<1, D, EPI>(p, lds, w0, w1, r0, r1, rot, off, ne, mc, n0, split, lane);
+    }
+}
+
+// expert_out[sorted_slot[r], h] = fp16(((partial[0][r][h] + partial[1][r][h]) + ...)), 8 columns per thread.
+__global__ __launch_bounds__(256) void down_reduce_kernel(const float* __restrict__ partial,
+                                                          const int32_t* __restrict__ sorted_slot,
+                                                          const int32_t* __restrict__ offsets, int E, int total_rows,
+                                                          int H, int nsplit, uint16_t* __restrict__ expert_out) {
+    const int vec = H / 8;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (idx >= static_cast<int64_t>(total_rows) * vec) return;
+    const int r = static_cast<int>(idx / vec);
+    const int c = static_cast<int>(idx % vec) * 8;
+    if (r >= offsets[E]) return;  // rows past the valid ones (ids outside [0, E)) belong to no expert
+    float acc[8];
+    const float* src = partial + static_cast<size_t>(r) * H + c;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = src[j];
+    for (int s = 1; s < nsplit; ++s) {
+        const float* ps = src + static_cast<size_t>(s) * total_rows * H;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] += ps[j];
+    }
+    f16x8 o;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = static_cast<f16>(acc[j]);
+    *reinterpret_cast<f16x8*>(expert_out + static_cast<size_t>(sorted_slot[r]) * H + c) = o;
+}
+
+// K-range for one workgroup: the largest multiple of 32*D dividing kdim such that rows_cap rows of it (padded)
+// fit the LDS; deepest ring first. Sets kc, D, rows_cap.
+struct StreamShape {
+    int kc, d, rows_cap, nsplit;
+};
+
+StreamShape pick_shape(int kdim, bool allow_split) {
+    for (int rows_cap : {kMaxRows, 16}) {
+        const int kc_max = kLdsMax / (rows_cap * 2) - 8;
+        for (int d = 8; d >= 1; d /= 2) {
+            int best = 0;
+            for (int kc = 32 * d; kc <= kc_max && kc <= kdim; kc += 32 * d)
+                if (kdim % kc == 0) best = kc;
+            if (best > 0 && (allow_split || best == kdim)) return StreamShape{best, d, rows_cap, kdim / best};
+        }
+    }
+    return StreamShape{0, 0, 0, 0};  // no layout: the caller reports unsupported
+}
+
+template <int EPI>
+hipError_t launch_stream_epi(const StreamArgs& p, int d, int grid, hipStream_t stream) {
+    const size_t lds = static_cast<size_t>(p.rows_cap) * (p.kc + 8) * sizeof(uint16_t);
+    hipError_t err = hipSuccess;
+#define MOE_STREAM_CASE(DEPTH)                                                                                 \
+    case DEPTH: {                                                                                              \
+        static const hipError_t attr = hipFuncSetAttribute(                                                    \
+            reinterpret_cast<const void*>(&ffn_stream_kernel<DEPTH, EPI>),                                     \
+            hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax);                                              \
+        if (attr != hipSuccess) return attr;                                                                   \
+        ffn_stream_kernel<DEPTH, EPI><<<grid, kThreads, lds, stream>>>(p);                                     \
+        break;                                                                                                 \
+    }
+    switch (d) {
+        MOE_STREAM_CASE(8)
+        MOE_STREAM_CASE(4)
+        MOE_STREAM_CASE(2)
+        MOE_STREAM_CASE(1)
+        default: return hipErrorInvalidValue;
+    }
+#undef MOE_STREAM_CASE
+    err = hipGetLastError();
+    return err;
+}
+
+}  // namespace
+
+int stream_block_threads() { return kThreads; }
+int stream_rows_per_pass() { return kMaxRows; }
+
+size_t stream_partial_bytes(int T, int H, int K, int I) {
+    const StreamShape s = pick_shape(I, true);
+    if (s.nsplit <= 1) return 0;
+    return static_cast<size_t>(s.nsplit) * T * K * H * sizeof(float);
+}
+
+bool stream_supported(int H, int I) { return pick_shape(H, false).kc > 0 && pick_shape(I, true).kc > 0; }
+
+int stream_gateup_grid(int E, int H, int I) {
+    (void)H;
+    return E * ((I + kWaves * 16 - 1) / (kWaves * 16));
+}
+
+int stream_down_grid(int E, int H, int I) {
+    return E * ((H + kWaves * 32 - 1) / (kWaves * 32)) * pick_shape(I, true).nsplit;
+}
+
+hipError_t launch_ffn_stream(const uint16_t* x, const uint16_t* expert_weights, uint16_t* expert_out,
+                             const FfnWorkspace& ws, int T, int H, int E, int K, int I, hipStream_t stream) {
+    StreamArgs p{};
+    p.sorted_slot = ws.sorted_slot;
+    p.offsets = ws.offsets;
+    p.w = expert_weights;
+    p.K = K;
+    p.H = H;
+    p.I = I;
+    p.total_rows = T * K;
+    // gate/up + SwiGLU: activations = gathered x rows, tiles = W_gate and W_up rows, out = hidden
+    const StreamShape gu = pick_shape(H, false);
+    p.act = x;
+    p.out = ws.hidden;
+    p.kdim = H;
+    p.ndim = I;
+    p.kc = gu.kc;
+    p.rows_cap = gu.rows_cap;
+    p.nsplit = 1;
+    p.w_off = 0;
+    p.w1_off = static_cast<size_t>(I) * H;
+    p.gather = 1;
+    hipError_t err;
+    {
+        TraceScope trace("moe_ffn_gateup_swiglu", stream);
+        err = launch_stream_epi<kSwiGLU>(p, gu.d, stream_gateup_grid(E, H, I), stream);
+    }
+    if (err != hipSuccess) return err;
+    // down: activations = hidden rows, tiles = W_down rows n0..n0+15 and n0+16..n0+31
+    const StreamShape dn = pick_shape(I, true);
+    p.act = ws.hidden;
+    p.out = expert_out;
+    p.partial = ws.partial;
+    p.kdim = I;
+    p.ndim = H;
+    p.kc = dn.kc;
+    p.rows_cap = dn.rows_cap;
+    p.nsplit = dn.nsplit;
+    p.w_off = 2 * static_cast<size_t>(I) * H;
+    p.w1_off = static_cast<size_t>(16) * I;
+    p.gather = 0;
+    {
+        TraceScope trace("moe_ffn_down", stream);
+        err = dn.nsplit > 1 ? launch_stream_epi<kPartial>(p, dn.d, stream_down_grid(E, H, I), stream)
+                            : launch_stream_epi<kScatter>(p, dn.d, stream_down_grid(E, H, I), stream);
+    }
+    if (err != hipSuccess || dn.nsplit <= 1) return err;
+    {
+        TraceScope trace("moe_ffn_down_reduce", stream);
+        const int64_t work = static_cast<int64_t>(T) * K * (H / 8);
+        down_reduce_kernel<<<static_cast<int>((work + 255) / 256), 256, 0, stream>>>(
+            ws.partial, ws.sorted_slot, ws.offsets, E, T * K, H, dn.nsplit, expert_out);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace moe

@@ -34,9 +34,10 @@ struct FfnWorkspace {
     int32_t* offsets;      // [E + 1] first sorted row of each expert; offsets[E] = number of valid slots
     int32_t* sorted_slot;  // [T*K]   slot index t*K + k of each sorted row, experts ascending, slots ascending
     uint16_t* hidden;      // [T*K, I] fp16 SwiGLU intermediate, rows in sorted order
+    float* partial;        // [nsplit, T*K, H] fp32 split-K partial sums of the down projection (may be empty)
 };
-size_t ffn_workspace_bytes(int64_t T, int64_t E, int64_t K, int64_t I);
-FfnWorkspace ffn_workspace_carve(void* base, int64_t T, int64_t E, int64_t K, int64_t I);
+size_t ffn_workspace_bytes(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I);
+FfnWorkspace ffn_workspace_carve(void* base, int64_t T, int64_t H, int64_t E, int64_t K, int64_t I);
 
 int permute_block_threads();
 hipError_t launch_permute(const int32_t* ids, int S, int E, int H, FfnWorkspace ws, uint16_t* expert_out,
@@ -50,6 +51,15 @@ struct FfnGrid {
     int schedule;
 };
 FfnGrid ffn_grid(int T, int H, int E, int K, int I);
+// weight-streaming schedule (moe_ffn_stream.hip)
+int stream_block_threads();
+int stream_rows_per_pass();
+bool stream_supported(int H, int I);
+size_t stream_partial_bytes(int T, int H, int K, int I);
+int stream_gateup_grid(int E, int H, int I);
+int stream_down_grid(int E, int H, int I);
+hipError_t launch_ffn_stream(const uint16_t* x, const uint16_t* expert_weights, uint16_t* expert_out,
+                             const FfnWorkspace& ws, int T, int H, int E, int K, int I, hipStream_t stream);
 hipError_t launch_ffn(const uint16_t* x, const uint16_t* expert_weights, uint16_t* expert_out, FfnWorkspace ws,
                       int T, int H, int E, int K, int I, hipStream_t stream);
 

@@ -59,6 +59,8 @@ moe_status check_ffn_sizes(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I
     if (st != MOE_OK) return st;
     if (I <= 0) return fail(MOE_ERR_ARG, "intermediateSize=%lld must be > 0", (long long)I);
     if (I % 32 != 0) return fail(MOE_ERR_UNSUPPORTED, "intermediateSize=%lld must be a multiple of 32", (long long)I);
+    if (!moe::stream_supported(static_cast<int>(H), static_cast<int>(I)))
+        return fail(MOE_ERR_UNSUPPORTED, "hiddenSize=%lld too large for the LDS-staged expert GEMMs", (long long)H);
     if (T * K * I > kInt32Max * 64LL) return fail(MOE_ERR_UNSUPPORTED, "T*K*I too large");
     return ok();
 }
@@ -201,7 +203,7 @@ moe_status moe_expert_ffn_infer_dtype(moe_dtype* expert_out_dtype) {
 
 size_t moe_expert_ffn_workspace_bytes(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
     if (check_ffn_sizes(T, H, E, K, I) != MOE_OK) return 0;
-    return moe::ffn_workspace_bytes(T, E, K, I);
+    return moe::ffn_workspace_bytes(T, H, E, K, I);
 }
 
 moe_status moe_expert_ffn_plan(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I, moe_ffn_plan* plan) {
@@ -221,7 +223,7 @@ moe_status moe_expert_ffn_plan(int64_t T, int64_t H, int64_t E, int64_t K, int64
     plan->down_grid = g.down_blocks;
     plan->block = g.block_threads;
     plan->rows_per_tile = g.rows_per_tile;
-    plan->workspace_bytes = moe::ffn_workspace_bytes(T, E, K, I);
+    plan->workspace_bytes = moe::ffn_workspace_bytes(T, H, E, K, I);
     return ok();
 }
 
@@ -235,14 +237,14 @@ moe_status moe_expert_ffn(const uint16_t* x, const int32_t* expert_ids, const ui
     if (T == 0) return ok();
     if (!x || !expert_ids || !expert_weights || !expert_out)
         return fail(MOE_ERR_NULL, "MoeExpertFFN: null tensor pointer");
-    const size_t need = moe::ffn_workspace_bytes(T, E, K, I);
+    const size_t need = moe::ffn_workspace_bytes(T, H, E, K, I);
     if (!workspace || workspace_bytes < need)
         return fail(MOE_ERR_WORKSPACE, "MoeExpertFFN: workspace %zu bytes at %p, need %zu", workspace_bytes,
                     workspace, need);
     if (!aligned16(x) || !aligned16(expert_weights) || !aligned16(expert_out) || !aligned16(workspace))
         return fail(MOE_ERR_UNSUPPORTED, "MoeExpertFFN: x, expert_weights, expert_out, workspace must be 16-byte aligned");
     const hipStream_t s = as_stream(stream);
-    const moe::FfnWorkspace ws = moe::ffn_workspace_carve(workspace, T, E, K, I);
+    const moe::FfnWorkspace ws = moe::ffn_workspace_carve(workspace, T, H, E, K, I);
     hipError_t err = moe::launch_permute(expert_ids, static_cast<int>(T * K), static_cast<int>(E), static_cast<int>(H),
                                          ws, expert_out, s);
     if (err != hipSuccess) return hip_fail(err, "MoeExpertFFN permute launch");

@@ -102,8 +102,9 @@ def test_plans(lib):
     assert lib.moe_expert_ffn_plan(128, 2048, 16, 2, 8192, C.byref(fp)) == MOE_OK
     ws = lib.moe_expert_ffn_workspace_bytes(128, 2048, 16, 2, 8192)
     assert fp.workspace_bytes == ws
-    # offsets + sorted slots + the fp16 [T*K, I] intermediate, each 256-byte aligned
-    assert ws == 256 + 1024 + 128 * 2 * 8192 * 2
+    # offsets + sorted slots + the fp16 [T*K, I] intermediate + fp32 split-K partials of the down projection
+    # (I = 8192 is split into 4 K-ranges of 2048), each 256-byte aligned
+    assert ws == 256 + 1024 + 128 * 2 * 8192 * 2 + 4 * 128 * 2 * 2048 * 4
     assert fp.permute_grid == 16 and fp.gateup_grid > 0 and fp.down_grid > 0
     assert lib.moe_expert_ffn_workspace_bytes(128, 2048, 16, 2, 8200) == 0  # I % 32 != 0
     assert lib.moe_expert_ffn_plan(16384, 2048, 64, 6, 1408, C.byref(fp)) == MOE_OK
