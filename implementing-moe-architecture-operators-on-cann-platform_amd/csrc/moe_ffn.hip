@@ -5,7 +5,10 @@
 //   moe_permute.hip      expert-sorted slot order + per-expert offsets (workspace)
 //   gate/up + SwiGLU     hidden[r, :] = silu(x_t W_gate_e^T) * (x_t W_up_e^T) for sorted row r = (t, k), fp16
 //   down + scatter       expert_out[t, k, :] = hidden[r, :] W_down_e^T, fp16
-// The grouped GEMMs have two schedules (moe_ffn_stream.hip: weight streaming for few rows per expert).
+// The grouped GEMMs have two schedules, chosen on the host from the average number of rows per expert
+// (the actual per-expert counts exist only on the device):
+//   moe_ffn_stream.hip  weight streaming, for few rows per expert (HBM-bound: every weight byte read once)
+//   moe_ffn_tiled.hip   256x256 LDS-tiled MFMA tiles, for many rows per expert (MFMA-bound)
 
 #include "moe_device.h"
 #include "moe_launch.h"
@@ -16,7 +19,18 @@ namespace {
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+constexpr int64_t kTiledMinRowsPerExpert = 64;
+
 }  // namespace
+
+int ffn_schedule(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
+    const bool stream_ok = stream_supported(static_cast<int>(H), static_cast<int>(I));
+    const bool tiled_ok = tiled_supported(static_cast<int>(H), static_cast<int>(I));
+    const bool many_rows = T * K >= kTiledMinRowsPerExpert * E;
+    if (tiled_ok && (many_rows || !stream_ok)) return 1;
+    if (stream_ok) return 0;
+    return -1;
+}
 
 // Layout (each region 256-byte aligned): offsets [E+1] i32 | sorted_slot [T*K] i32 | hidden [T*K, I] fp16 |
 // partial [nsplit, T*K, H] fp32 (only when the down projection is split over K).
@@ -25,8 +39,9 @@ size_t ffn_workspace_bytes(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I
     size_t bytes = align_up(sizeof(int32_t) * static_cast<size_t>(E + 1), 256);
     bytes += align_up(sizeof(int32_t) * S, 256);
     bytes += align_up(sizeof(uint16_t) * S * static_cast<size_t>(I), 256);
-    bytes += align_up(stream_partial_bytes(static_cast<int>(T), static_cast<int>(H), static_cast<int>(K),
-                                           static_cast<int>(I)), 256);
+    if (ffn_schedule(T, H, E, K, I) == 0)
+        bytes += align_up(stream_partial_bytes(static_cast<int>(T), static_cast<int>(H), static_cast<int>(K),
+                                               static_cast<int>(I)), 256);
     return bytes;
 }
 
@@ -46,20 +61,29 @@ FfnWorkspace ffn_workspace_carve(void* base, int64_t T, int64_t H, int64_t E, in
 }
 
 FfnGrid ffn_grid(int T, int H, int E, int K, int I) {
-    (void)T;
-    (void)K;
     FfnGrid g;
-    g.schedule = 0;
-    g.block_threads = stream_block_threads();
-    g.gateup_blocks = stream_gateup_grid(E, H, I);
-    g.down_blocks = stream_down_grid(E, H, I);
-    g.rows_per_tile = stream_rows_per_pass();
+    g.schedule = ffn_schedule(T, H, E, K, I);
+    if (g.schedule == 1) {
+        g.block_threads = tiled_block_threads();
+        g.gateup_blocks = tiled_gateup_grid(T, E, K, I);
+        g.down_blocks = tiled_down_grid(T, E, K, H);
+        g.rows_per_tile = tiled_rows_per_tile();
+    } else {
+        g.block_threads = stream_block_threads();
+        g.gateup_blocks = stream_gateup_grid(E, H, I);
+        g.down_blocks = stream_down_grid(E, H, I);
+        g.rows_per_tile = stream_rows_per_pass();
+    }
     return g;
 }
 
 hipError_t launch_ffn(const uint16_t* x, const uint16_t* expert_weights, uint16_t* expert_out, FfnWorkspace ws,
                       int T, int H, int E, int K, int I, hipStream_t stream) {
-    return launch_ffn_stream(x, expert_weights, expert_out, ws, T, H, E, K, I, stream);
+    switch (ffn_schedule(T, H, E, K, I)) {
+        case 1: return launch_ffn_tiled(x, expert_weights, expert_out, ws, T, H, E, K, I, stream);
+        case 0: return launch_ffn_stream(x, expert_weights, expert_out, ws, T, H, E, K, I, stream);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace moe

@@ -1,0 +1,264 @@
+// moe_ffn_tiled.hip -- LDS-tiled schedule of the MoeExpertFFN grouped GEMMs (many rows per expert, prefill).
+//
+// Reference: op_kernel/moe_expert_ffn.cpp (ComputeSwiGLU :265-333, ComputeDownProj :339-394, scatter :250-257);
+// oracle: tests/moe_cpu_sim.cpp:245-296 (W_gate, W_up [I, H]; W_down [H, I]).
+//
+// With ~1000 rows per expert (T = 8192, K = 2, E = 16) the GEMMs are MFMA-bound. Both are "NT": activation rows
+// and weight rows are contiguous along the reduction dim k.
+//   macro tile   256 activation rows x 256 weight rows x 64 k per stage; 4 waves, each a 128 x 128 sub-tile
+//                (8 x 8 v_mfma_f32_16x16x32_f16 tiles, 256 fp32 accumulators per lane)
+//   pipeline     the next stage's 16 x 16 B per thread are loaded into registers while the current stage is
+//                multiplied out of LDS; two LDS stages (row pitch 64 + 8 halfs: the 16 rows of one ds_read_b128
+//                fall in different banks), one barrier per stage
+//   gate/up      the 256 weight rows of a tile are, per wave half, 64 W_gate rows and the matching 64 W_up rows,
+//                so each wave holds gate and up of the same (row, i) and applies SwiGLU in registers, writing
+//                fp16 hidden rows
+//   down         weight rows are W_down rows (output columns); the epilogue writes expert_out[slot] directly
+//   scheduling   tiles are (expert, n-tile, m-tile) with m fastest, numbered from the per-expert row counts
+//                at run time; the grid is an upper bound and surplus workgroups exit. Workgroups are dispatched
+//                round-robin over the 8 XCDs, so the linear tile order is remapped to give each XCD a
+//                contiguous range: the m-tiles that share a weight tile then share that XCD's L2.
+// Rows past an expert's count are clamped to its last row on load and masked on store.
+
+#include "moe_device.h"
+#include "moe_launch.h"
+
+namespace moe {
+
+namespace {
+
+constexpr int kBM = 256;           // activation rows per tile
+constexpr int kBN = 256;           // weight rows per tile
+constexpr int kBK = 64;            // k per stage
+constexpr int kPitch = kBK + 8;    // LDS row pitch in halfs
+constexpr int kThreads = 256;      // 4 waves
+constexpr int kStageHalfs = (kBM + kBN) * kPitch;
+constexpr int kLdsBytes = 2 * kStageHalfs * 2;  // 147456
+constexpr int kXcds = 8;
+
+enum Epilogue { kSwiGLU = 0, kScatter = 1 };
+
+struct TiledArgs {
+    const uint16_t* act;         // x [T, H] (gate/up, gathered) or hidden [T*K, I] (down)
+    const int32_t* sorted_slot;
+    const int32_t* offsets;
+    const uint16_t* w;           // expert_weights
+    uint16_t* out;               // hidden or expert_out
+    int E, K, H, I;
+    int kdim;                    // H or I
+    int ndim;                    // I (gate/up: tile covers 128 i of gate and up) or H (down)
+    int ntiles_n;                // n-tiles per expert
+    int gather;                  // gate/up: activation row r -> x[sorted_slot[r] / K]
+};
+
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+__device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)); }
+
+// Linear tile -> (expert, m-tile, n-tile); false when t is past the last tile.
+__device__ __forceinline__ bool find_tile(const TiledArgs& p, int t, int* e_out, int* mt_out, int* nt_out,
+                                          int* off_out, int* ne_out) {
+    int base = 0;
+    for (int e = 0; e < p.E; ++e) {
+        const int off = p.offsets[e];
+        const int ne = p.offsets[e + 1] - off;
+        const int mtiles = (ne + kBM - 1) / kBM;
+        const int tiles = mtiles * p.ntiles_n;
+        if (t < base + tiles) {
+            const int local = t - base;
+            *e_out = e;
+            *nt_out = local / mtiles;
+            *mt_out = local % mtiles;
+            *off_out = off;
+            *ne_out = ne;
+            return true;
+        }
+        base += tiles;
+    }
+    return false;
+}
+
+template <int EPI>
+__global__ __launch_bounds__(kThreads) void ffn_tiled_kernel(TiledArgs p) {
+    extern __shared__ __align__(16) uint16_t lds[];
+    // XCD-contiguous remap of the dispatch order
+    const int G = static_cast<int>(gridDim.x);
+    const int per_xcd = (G + kXcds - 1) / kXcds;
+    const int b = static_cast<int>(blockIdx.x);
+    const int t = (b % kXcds) * per_xcd + b / kXcds;
+    int e, mt, nt, off, ne;
+    if (!find_tile(p, t, &e, &mt, &nt, &off, &ne)) return;
+
+    const int tid = static_cast<int>(threadIdx.x);
+    const int wave = tid / kWave;
+    const int lane = lane_id();
+    const int row16 = lane & 15, kg = lane >> 4;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = mt * kBM;
+    const size_t ebase = static_cast<size_t>(e) * 3 * static_cast<size_t>(p.I) * p.H;
+
+    // ---- per-thread global load plan: rows (tid / 8) + 32 j, k-granule tid % 8 (16 B) ----
+    const int kgr = tid & 7;
+    const uint16_t* arow[8];
+    const uint16_t* brow[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int r = (tid >> 3) + 32 * j;  // 0..255
+        const int m = min(m0 + r, ne - 1);
+        const size_t src = p.gather ? static_cast<size_t>(p.sorted_slot[off + m] / p.K) : static_cast<size_t>(off + m);
+        arow[j] = p.act + src * p.kdim + kgr * 8;
+        size_t wrow;
+        if (EPI == kSwiGLU) {
+            // tile row r: wave half r/128; within it 64 gate rows then the 64 matching up rows
+            const int half = r >> 7, sub = r & 127;
+            const int i = nt * 128 + half * 64 + (sub & 63);
+            const int ic = min(i, p.I - 1);
+            wrow = (sub < 64 ? 0 : static_cast<size_t>(p.I) * p.H) + static_cast<size_t>(ic) * p.H;
+        } else {
+            const int n = min(nt * kBN + r, p.H - 1);
+            wrow = 2 * static_cast<size_t>(p.I) * p.H + static_cast<size_t>(n) * p.I;
+        }
+        brow[j] = p.w + ebase + wrow + kgr * 8;
+    }
+
+    f32x4 acc[8][8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    u32x4 ga[8], gb[8];
+    auto load_stage = [&](int ks) {
+        const int k0 = ks * kBK;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ga[j] = *reinterpret_cast<const u32x4*>(arow[j] + k0);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) gb[j] = *reinterpret_cast<const u32x4*>(brow[j] + k0);
+    };
+    auto store_stage = [&](int buf) {
+        uint16_t* sa = lds + buf * kStageHalfs;
+        uint16_t* sb = sa + kBM * kPitch;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int r = (tid >> 3) + 32 * j;
+            *reinterpret_cast<u32x4*>(sa + r * kPitch + kgr * 8) = ga[j];
+            *reinterpret_cast<u32x4*>(sb + r * kPitch + kgr * 8) = gb[j];
+        }
+    };
+
+    const int nstages = p.kdim / kBK;
+    load_stage(0);
+    store_stage(0);
+    lds_barrier();
+    for (int s = 0; s < nstages; ++s) {
+        const int buf = s & 1;
+        if (s + 1 < nstages) load_stage(s + 1);
+        const uint16_t* sa = lds + buf * kStageHalfs + (wm * 128) * kPitch;
+        const uint16_t* sb = lds + buf * kStageHalfs + kBM * kPitch + (wn * 128) * kPitch;
+#pragma unroll
+        for (int kk = 0; kk < kBK / 32; ++kk) {
+            f16x8 af[8], bf[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                af[i] = *reinterpret_cast<const f16x8*>(sa + (i * 16 + row16) * kPitch + kk * 32 + kg * 8);
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                bf[j] = *reinterpret_cast<const f16x8*>(sb + (j * 16 + row16) * kPitch + kk * 32 + kg * 8);
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[i][j] = mfma16x16x32(af[i], bf[j], acc[i][j]);
+        }
+        if (s + 1 < nstages) store_stage(buf ^ 1);
+        lds_barrier();
+    }
+
+    // ---- epilogue: acc[i][j] lane holds D[m = 4*kg + r][n = row16] of sub-tile (i, j) ----
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int m = m0 + wm * 128 + i * 16 + kg * 4 + r;
+            if (m >= ne) continue;
+            if (EPI == kSwiGLU) {
+                uint16_t* dst = p.out + static_cast<size_t>(off + m) * p.I;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int col = nt * 128 + wn * 64 + j * 16 + row16;
+                    if (col < p.I) dst[col] = f32_to_f16_bits(silu_f32(acc[i][j][r]) * acc[i][j + 4][r]);
+                }
+            } else {
+                uint16_t* dst = p.out + static_cast<size_t>(p.sorted_slot[off + m]) * p.H;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int col = nt * kBN + wn * 128 + j * 16 + row16;
+                    if (col < p.H) dst[col] = f32_to_f16_bits(acc[i][j][r]);
+                }
+            }
+        }
+}
+
+template <int EPI>
+hipError_t launch_tiled(const TiledArgs& p, int grid, hipStream_t stream) {
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&ffn_tiled_kernel<EPI>),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+    if (attr != hipSuccess) return attr;
+    ffn_tiled_kernel<EPI><<<grid, kThreads, kLdsBytes, stream>>>(p);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool tiled_supported(int H, int I) { return H % kBK == 0 && I % kBK == 0; }
+int tiled_block_threads() { return kThreads; }
+int tiled_rows_per_tile() { return kBM; }
+// Upper bound on the tile count (sum over experts of ceil(rows_e / kBM) <= ceil(T*K / kBM) + E), rounded up to
+// a multiple of the XCD count so that the XCD-contiguous remap in the kernel is a bijection on [0, grid).
+int tiled_grid(int T, int E, int K, int ntiles_n) {
+    const int m_bound = (T * K + kBM - 1) / kBM + E;
+    const int g = m_bound * ntiles_n;
+    return (g + kXcds - 1) / kXcds * kXcds;
+}
+int tiled_gateup_grid(int T, int E, int K, int I) { return tiled_grid(T, E, K, (I + 127) / 128); }
+int tiled_down_grid(int T, int E, int K, int H) { return tiled_grid(T, E, K, (H + kBN - 1) / kBN); }
+
+hipError_t launch_ffn_tiled(const uint16_t* x, const uint16_t* expert_weights, uint16_t* expert_out,
+                            const FfnWorkspace& ws, int T, int H, int E, int K, int I, hipStream_t stream) {
+    TiledArgs p{};
+    p.sorted_slot = ws.sorted_slot;
+    p.offsets = ws.offsets;
+    p.w = expert_weights;
+    p.E = E;
+    p.K = K;
+    p.H = H;
+    p.I = I;
+    p.act = x;
+    p.out = ws.hidden;
+    p.kdim = H;
+    p.ndim = I;
+    p.ntiles_n = (I + 127) / 128;
+    p.gather = 1;
+    hipError_t err;
+    {
+        TraceScope trace("moe_ffn_gateup_swiglu", stream);
+        err = launch_tiled<kSwiGLU>(p, tiled_gateup_grid(T, E, K, I), stream);
+    }
+    if (err != hipSuccess) return err;
+    p.act = ws.hidden;
+    p.out = expert_out;
+    p.kdim = I;
+    p.ndim = H;
+    p.ntiles_n = (H + kBN - 1) / kBN;
+    p.gather = 0;
+    {
+        TraceScope trace("moe_ffn_down", stream);
+        err = launch_tiled<kScatter>(p, tiled_down_grid(T, E, K, H), stream);
+    }
+    return err;
+}
+
+}  // namespace moe

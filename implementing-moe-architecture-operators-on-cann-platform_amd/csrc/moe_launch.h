@@ -60,6 +60,16 @@ int stream_gateup_grid(int E, int H, int I);
 int stream_down_grid(int E, int H, int I);
 hipError_t launch_ffn_stream(const uint16_t* x, const uint16_t* expert_weights, uint16_t* expert_out,
                              const FfnWorkspace& ws, int T, int H, int E, int K, int I, hipStream_t stream);
+// LDS-tiled schedule (moe_ffn_tiled.hip)
+bool tiled_supported(int H, int I);
+int tiled_block_threads();
+int tiled_rows_per_tile();
+int tiled_gateup_grid(int T, int E, int K, int I);
+int tiled_down_grid(int T, int E, int K, int H);
+hipError_t launch_ffn_tiled(const uint16_t* x, const uint16_t* expert_weights, uint16_t* expert_out,
+                            const FfnWorkspace& ws, int T, int H, int E, int K, int I, hipStream_t stream);
+// schedule choice: 0 = weight streaming, 1 = LDS-tiled, -1 = no kernel supports the shape
+int ffn_schedule(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I);
 hipError_t launch_ffn(const uint16_t* x, const uint16_t* expert_weights, uint16_t* expert_out, FfnWorkspace ws,
                       int T, int H, int E, int K, int I, hipStream_t stream);
 

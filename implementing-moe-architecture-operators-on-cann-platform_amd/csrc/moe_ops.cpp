@@ -59,8 +59,9 @@ moe_status check_ffn_sizes(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I
     if (st != MOE_OK) return st;
     if (I <= 0) return fail(MOE_ERR_ARG, "intermediateSize=%lld must be > 0", (long long)I);
     if (I % 32 != 0) return fail(MOE_ERR_UNSUPPORTED, "intermediateSize=%lld must be a multiple of 32", (long long)I);
-    if (!moe::stream_supported(static_cast<int>(H), static_cast<int>(I)))
-        return fail(MOE_ERR_UNSUPPORTED, "hiddenSize=%lld too large for the LDS-staged expert GEMMs", (long long)H);
+    if (moe::ffn_schedule(T, H, E, K, I) < 0)
+        return fail(MOE_ERR_UNSUPPORTED, "hiddenSize=%lld / intermediateSize=%lld: no expert GEMM schedule fits",
+                    (long long)H, (long long)I);
     if (T * K * I > kInt32Max * 64LL) return fail(MOE_ERR_UNSUPPORTED, "T*K*I too large");
     return ok();
 }

@@ -288,3 +288,44 @@ def test_baseline_config_sampled(ops, name):
     y_chk = oracle.combine(f32(host(eo_d)), f32(w)).astype(np.float16)
     assert np.array_equal(y_all.view(np.uint16), y_chk.view(np.uint16))
     assert np.isfinite(f32(y_all)).all()
+
+
+def ffn_schedule(T, H, E, K, I) -> int:
+    import ctypes as C
+
+    from conftest import package
+
+    lib_mod = package()._lib
+    plan = lib_mod.FfnPlan()
+    assert lib_mod.load().moe_expert_ffn_plan(T, H, E, K, I, C.byref(plan)) == 0
+    return plan.schedule
+
+
+@pytest.mark.parametrize("T,H,E,K,I", [
+    (300, 128, 4, 2, 128),    # partial m-tiles (~150 rows per expert)
+    (257, 320, 3, 2, 192),    # partial n-tiles in both GEMMs (I = 192 -> 2 x 128, H = 320 -> 2 x 256)
+    (600, 64, 8, 3, 64),      # K = 3, single k-stage
+    (700, 192, 2, 1, 1408),   # >256 rows per expert (several m-tiles), DeepSeek's I
+])
+def test_ffn_tiled_schedule_full_oracle(ops, T, H, E, K, I):
+    assert ffn_schedule(T, H, E, K, I) == 1
+    rng = np.random.default_rng(T + H + I)
+    x = rng.standard_normal((T, H)).astype(np.float16)
+    ew = np.concatenate([rng.standard_normal((E, 2 * I, H)) / math.sqrt(H),
+                         rng.standard_normal((E, I, H)) / math.sqrt(I)], axis=1).astype(np.float16)
+    ids = np.stack([rng.permutation(E)[:K] for _ in range(T)]).astype(np.int32)
+    w = np.full((T, K), 1.0 / K, np.float16)
+    eo_d, ws = run_ffn(ops, dev(x), dev(ids), dev(w), dev(ew), I)
+    check_permute(host(ws), ids, E)
+    eo = f32(host(eo_d))
+    eo_o = oracle.expert_ffn(f32(x), ids, f32(ew), I)
+    m = oracle.compare(eo, eo_o)
+    log(f"[tiled T{T} H{H} E{E} K{K} I{I}] expert_out vs oracle: {m}")
+    within(m, max_abs=1e-2, mean_abs=1e-3, cos=0.9999)
+
+
+def test_decode_uses_streaming_and_prefill_uses_tiled():
+    assert ffn_schedule(128, 2048, 16, 2, 8192) == 0
+    assert ffn_schedule(8192, 2048, 16, 2, 8192) == 1
+    assert ffn_schedule(16384, 2048, 64, 6, 1408) == 1
+    assert ffn_schedule(4096, 4096, 8, 2, 14336) == 1
