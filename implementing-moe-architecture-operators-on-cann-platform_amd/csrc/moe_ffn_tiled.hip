@@ -5,14 +5,17 @@
 //
 // With ~1000 rows per expert (T = 8192, K = 2, E = 16) the GEMMs are MFMA-bound. Both are "NT": activation rows
 // and weight rows are contiguous along the reduction dim k.
-//   macro tile   256 activation rows x 256 weight rows x 64 k per stage; 4 waves, each a 128 x 128 sub-tile
-//                (8 x 8 v_mfma_f32_16x16x32_f16 tiles, 256 fp32 accumulators per lane)
-//   pipeline     the next stage's 16 x 16 B per thread are loaded into registers while the current stage is
-//                multiplied out of LDS; two LDS stages (row pitch 64 + 8 halfs: the 16 rows of one ds_read_b128
-//                fall in different banks), one barrier per stage
-//   gate/up      the 256 weight rows of a tile are, per wave half, 64 W_gate rows and the matching 64 W_up rows,
-//                so each wave holds gate and up of the same (row, i) and applies SwiGLU in registers, writing
-//                fp16 hidden rows
+//   macro tile   256 activation rows x 256 weight rows x 64 k per stage; 8 waves (2 x 4), each a 128 x 64
+//                sub-tile (8 x 4 v_mfma_f32_16x16x32_f16 tiles, 128 fp32 accumulators per lane: with 256 per
+//                lane the accumulators plus the loop's other live values exceed one wave's register file and
+//                the compiler shuffles them between register files every iteration)
+//   pipeline     the next stage's 8 x 16 B per thread are loaded into registers while the current stage is
+//                multiplied out of LDS; two LDS stages, one barrier per stage
+//   LDS layout   unpadded 128-byte rows of 8 granules of 16 B; granule g of row r is stored at g ^ ((r >> 1) & 7),
+//                so the 16 rows one ds_read_b128 touches (same logical granule) spread over all banks
+//   gate/up      the 256 weight rows of a tile are, per wave quarter, 32 W_gate rows and the matching 32 W_up
+//                rows, so each wave holds gate and up of the same (row, i) and applies SwiGLU in registers,
+//                writing fp16 hidden rows
 //   down         weight rows are W_down rows (output columns); the epilogue writes expert_out[slot] directly
 //   scheduling   tiles are (expert, n-tile, m-tile) with m fastest, numbered from the per-expert row counts
 //                at run time; the grid is an upper bound and surplus workgroups exit. Workgroups are dispatched
@@ -30,10 +33,10 @@ namespace {
 constexpr int kBM = 256;           // activation rows per tile
 constexpr int kBN = 256;           // weight rows per tile
 constexpr int kBK = 64;            // k per stage
-constexpr int kPitch = kBK + 8;    // LDS row pitch in halfs
-constexpr int kThreads = 256;      // 4 waves
+constexpr int kPitch = kBK;        // LDS row pitch in halfs (granules XOR-swizzled)
+constexpr int kThreads = 512;      // 8 waves
 constexpr int kStageHalfs = (kBM + kBN) * kPitch;
-constexpr int kLdsBytes = 2 * kStageHalfs * 2;  // 147456
+constexpr int kLdsBytes = 2 * kStageHalfs * 2;  // 131072
 constexpr int kXcds = 8;
 
 enum Epilogue { kSwiGLU = 0, kScatter = 1 };
@@ -97,56 +100,56 @@ __global__ __launch_bounds__(kThreads) void ffn_tiled_kernel(TiledArgs p) {
     const int wave = tid / kWave;
     const int lane = lane_id();
     const int row16 = lane & 15, kg = lane >> 4;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave >> 2, wn = wave & 3;  // 2 x 4 waves: rows wm*128.., weight rows wn*64..
     const int m0 = mt * kBM;
     const size_t ebase = static_cast<size_t>(e) * 3 * static_cast<size_t>(p.I) * p.H;
 
-    // ---- per-thread global load plan: rows (tid / 8) + 32 j, k-granule tid % 8 (16 B) ----
+    // ---- per-thread global load plan: rows (tid / 8) + 64 j, k-granule tid % 8 (16 B) ----
+    // 32-bit element offsets from uniform bases keep the vector-register budget for the accumulators.
     const int kgr = tid & 7;
-    const uint16_t* arow[8];
-    const uint16_t* brow[8];
+    const uint16_t* abase = p.act + kgr * 8;
+    const uint16_t* wbase = p.w + ebase + kgr * 8;
+    uint32_t aoff[4], boff[4];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int r = (tid >> 3) + 32 * j;  // 0..255
+    for (int j = 0; j < 4; ++j) {
+        const int r = (tid >> 3) + 64 * j;  // 0..255
         const int m = min(m0 + r, ne - 1);
-        const size_t src = p.gather ? static_cast<size_t>(p.sorted_slot[off + m] / p.K) : static_cast<size_t>(off + m);
-        arow[j] = p.act + src * p.kdim + kgr * 8;
-        size_t wrow;
+        const uint32_t src = p.gather ? static_cast<uint32_t>(p.sorted_slot[off + m] / p.K) : static_cast<uint32_t>(off + m);
+        aoff[j] = src * static_cast<uint32_t>(p.kdim);
         if (EPI == kSwiGLU) {
-            // tile row r: wave half r/128; within it 64 gate rows then the 64 matching up rows
-            const int half = r >> 7, sub = r & 127;
-            const int i = nt * 128 + half * 64 + (sub & 63);
-            const int ic = min(i, p.I - 1);
-            wrow = (sub < 64 ? 0 : static_cast<size_t>(p.I) * p.H) + static_cast<size_t>(ic) * p.H;
+            // tile row r: wave quarter r/64; within it 32 gate rows then the 32 matching up rows
+            const int quarter = r >> 6, sub = r & 63;
+            const int ic = min(nt * 128 + quarter * 32 + (sub & 31), p.I - 1);
+            boff[j] = (sub < 32 ? 0u : static_cast<uint32_t>(p.I) * p.H) + static_cast<uint32_t>(ic) * p.H;
         } else {
             const int n = min(nt * kBN + r, p.H - 1);
-            wrow = 2 * static_cast<size_t>(p.I) * p.H + static_cast<size_t>(n) * p.I;
+            boff[j] = 2u * static_cast<uint32_t>(p.I) * p.H + static_cast<uint32_t>(n) * p.I;
         }
-        brow[j] = p.w + ebase + wrow + kgr * 8;
     }
 
-    f32x4 acc[8][8];
+    f32x4 acc[8][4];
 #pragma unroll
     for (int i = 0; i < 8; ++i)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    u32x4 ga[8], gb[8];
+    u32x4 ga[4], gb[4];
     auto load_stage = [&](int ks) {
         const int k0 = ks * kBK;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) ga[j] = *reinterpret_cast<const u32x4*>(arow[j] + k0);
+        for (int j = 0; j < 4; ++j) ga[j] = *reinterpret_cast<const u32x4*>(abase + aoff[j] + k0);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) gb[j] = *reinterpret_cast<const u32x4*>(brow[j] + k0);
+        for (int j = 0; j < 4; ++j) gb[j] = *reinterpret_cast<const u32x4*>(wbase + boff[j] + k0);
     };
     auto store_stage = [&](int buf) {
         uint16_t* sa = lds + buf * kStageHalfs;
         uint16_t* sb = sa + kBM * kPitch;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int r = (tid >> 3) + 32 * j;
-            *reinterpret_cast<u32x4*>(sa + r * kPitch + kgr * 8) = ga[j];
-            *reinterpret_cast<u32x4*>(sb + r * kPitch + kgr * 8) = gb[j];
+        for (int j = 0; j < 4; ++j) {
+            const int r = (tid >> 3) + 64 * j;
+            const int pg = kgr ^ ((r >> 1) & 7);
+            *reinterpret_cast<u32x4*>(sa + r * kPitch + pg * 8) = ga[j];
+            *reinterpret_cast<u32x4*>(sb + r * kPitch + pg * 8) = gb[j];
         }
     };
 
@@ -157,21 +160,22 @@ __global__ __launch_bounds__(kThreads) void ffn_tiled_kernel(TiledArgs p) {
     for (int s = 0; s < nstages; ++s) {
         const int buf = s & 1;
         if (s + 1 < nstages) load_stage(s + 1);
-        const uint16_t* sa = lds + buf * kStageHalfs + (wm * 128) * kPitch;
-        const uint16_t* sb = lds + buf * kStageHalfs + kBM * kPitch + (wn * 128) * kPitch;
+        // row (16 i + row16) has swizzle ((row16 >> 1) & 7): the 16-row offsets leave it unchanged
+        const int sw = (row16 >> 1) & 7;
+        const uint16_t* sa = lds + buf * kStageHalfs + (wm * 128 + row16) * kPitch;
+        const uint16_t* sb = lds + buf * kStageHalfs + (kBM + wn * 64 + row16) * kPitch;
 #pragma unroll
         for (int kk = 0; kk < kBK / 32; ++kk) {
-            f16x8 af[8], bf[8];
+            const int gran = ((kk * 4 + kg) ^ sw) * 8;
+            f16x8 af[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
-                af[i] = *reinterpret_cast<const f16x8*>(sa + (i * 16 + row16) * kPitch + kk * 32 + kg * 8);
+            for (int i = 0; i < 8; ++i) af[i] = *reinterpret_cast<const f16x8*>(sa + i * 16 * kPitch + gran);
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
-                bf[j] = *reinterpret_cast<const f16x8*>(sb + (j * 16 + row16) * kPitch + kk * 32 + kg * 8);
+            for (int j = 0; j < 4; ++j) {
+                const f16x8 bf = *reinterpret_cast<const f16x8*>(sb + j * 16 * kPitch + gran);
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
-#pragma unroll
-                for (int j = 0; j < 8; ++j) acc[i][j] = mfma16x16x32(af[i], bf[j], acc[i][j]);
+                for (int i = 0; i < 8; ++i) acc[i][j] = mfma16x16x32(af[i], bf, acc[i][j]);
+            }
         }
         if (s + 1 < nstages) store_stage(buf ^ 1);
         lds_barrier();
@@ -187,15 +191,15 @@ __global__ __launch_bounds__(kThreads) void ffn_tiled_kernel(TiledArgs p) {
             if (EPI == kSwiGLU) {
                 uint16_t* dst = p.out + static_cast<size_t>(off + m) * p.I;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int col = nt * 128 + wn * 64 + j * 16 + row16;
-                    if (col < p.I) dst[col] = f32_to_f16_bits(silu_f32(acc[i][j][r]) * acc[i][j + 4][r]);
+                for (int j = 0; j < 2; ++j) {
+                    const int col = nt * 128 + wn * 32 + j * 16 + row16;
+                    if (col < p.I) dst[col] = f32_to_f16_bits(silu_f32(acc[i][j][r]) * acc[i][j + 2][r]);
                 }
             } else {
                 uint16_t* dst = p.out + static_cast<size_t>(p.sorted_slot[off + m]) * p.H;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int col = nt * kBN + wn * 128 + j * 16 + row16;
+                for (int j = 0; j < 4; ++j) {
+                    const int col = nt * kBN + wn * 64 + j * 16 + row16;
                     if (col < p.H) dst[col] = f32_to_f16_bits(acc[i][j][r]);
                 }
             }
