@@ -95,7 +95,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported (this build has no multi-GPU "
-              "path; see DESIGN.md for how the layer would shard)", file=sys.stderr)
+              "path: expert-parallel sharding with an all-to-all on each side of the FFN is designed, not built)",
+              file=sys.stderr)
         return 2
 
     import numpy as np
