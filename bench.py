@@ -82,6 +82,30 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
+def calibrate_copy(ops, torch, args) -> int:
+    """Copy a known number of bytes HBM -> HBM (buffers far larger than the 256 MB Infinity Cache would not be
+    needed: the destination is written once and the source read once per launch). A counter run over this mode
+    gives the factor that turns FETCH_SIZE / WRITE_SIZE readings into bytes."""
+    nbytes = args.calibrate_copy << 20
+    dev = torch.device("cuda:0")
+    src = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    dst = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    src.fill_(1)
+    for _ in range(args.warmup):
+        ops.copy_bytes_(dst, src)
+    torch.cuda.synchronize()
+    with ops.kernel_trace() as kernels:
+        for _ in range(args.steps):
+            ops.copy_bytes_(dst, src)
+        torch.cuda.synchronize()
+    name, (launches, total_ms) = next(iter(kernels.items()))
+    avg_ms = total_ms / launches
+    print(json.dumps({"mode": "copy calibration", "kernel": name, "bytes_read": nbytes, "bytes_written": nbytes,
+                      "launches": launches, "avg_us": round(avg_ms * 1e3, 2),
+                      "GB/s (read + write)": round(2 * nbytes / (avg_ms * 1e-3) / 1e9, 1)}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -92,6 +116,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the reference CPU timing")
     ap.add_argument("--cpu-target-gflop", type=float, default=30.0,
                     help="size of the CPU baseline sample in GFLOP of expert FFN work")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="instead of the layer, run moe_copy_bytes over MIB MiB (reference for HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported (this build has no multi-GPU "
@@ -105,6 +131,8 @@ def main() -> int:
     ops = importlib.import_module(f"{PKG}.ops")
     synth = importlib.import_module(f"{PKG}.synth")
     lib = importlib.import_module(PKG).load_library()
+    if args.calibrate_copy:
+        return calibrate_copy(ops, torch, args)
     cfg = synth.CONFIGS[args.config]
     T, H, E, K, I = cfg.T, cfg.H, cfg.E, cfg.K, cfg.I
     dev = torch.device("cuda:0")
@@ -163,7 +191,7 @@ def main() -> int:
         per_kernel[name] = {"launches": launches, "avg_us": round(avg * 1e3, 2),
                             "GB/s": round(b / (avg * 1e-3) / 1e9, 1) if b else None,
                             "TFLOP/s": round(f / (avg * 1e-3) / 1e12, 2) if f else None}
-    ffn_names = ("moe_permute", "moe_ffn_gateup_swiglu", "moe_ffn_down")
+    ffn_names = ("moe_permute", "moe_ffn_gateup_swiglu", "moe_ffn_down", "moe_ffn_down_reduce")
     ffn_ms = sum(kernels[n][1] / kernels[n][0] for n in ffn_names if n in kernels)
     ffn_flops = 6 * T * K * H * I
     ffn_bytes = active * 3 * I * H * 2 + T * H * 2 + T * K * H * 2
