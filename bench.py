@@ -7,8 +7,12 @@ T=128, H=2048, E=16, K=2, I=8192 (fp16 I/O, fp32 accumulation) by default.
 A step is one pass of the layer over one batch of synthetic input resident in HBM: routing, the expert FFN
 (permute + fused gate/up/SwiGLU grouped GEMM + down grouped GEMM with the expert_out scatter) and combine, all
 through the C ABI of libmoe_mi355x.so on one stream, with caller-owned buffers allocated once.
-W warm-up steps, then K timed steps between torch.cuda.synchronize() calls; per-kernel durations come from
-HIP events that the library records around each of its launches on that same stream during the timed steps.
+W warm-up steps, then three timed passes of K steps each, every pass between torch.cuda.synchronize() calls:
+  1. eager: the three C-ABI calls per step, nothing else recorded -> `value` and `ms_per_step`;
+  2. graph replay: the same three calls captured once in a HIP graph, replayed K times (y checked bit-exact
+     against the eager y first) -> `layer_us_graph_replay`;
+  3. traced: eager again, with HIP events that the library records around each of its launches on the launch
+     stream -> per-kernel average durations, from which `roofline` is computed.
 
 The JSON line also carries:
   roofline      the dominant kernel's algorithmic bytes (or flops) per launch / its average event-timed
@@ -116,6 +120,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the reference CPU timing")
     ap.add_argument("--cpu-target-gflop", type=float, default=30.0,
                     help="size of the CPU baseline sample in GFLOP of expert FFN work")
+    ap.add_argument("--no-graph", action="store_true", help="skip the HIP-graph replay timing")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="instead of the layer, run moe_copy_bytes over MIB MiB (reference for HBM byte counters)")
     args = ap.parse_args()
@@ -155,31 +160,54 @@ def main() -> int:
     sp = int(stream.cuda_stream)
     p = {k: t.data_ptr() for k, t in dict(x=x, wg=wg, ew=ew, ids=ids, w=w, eo=eo, y=y, ws=ws).items()}
 
-    def step() -> None:
-        st = lib.moe_routing_topk(p["x"], p["wg"], p["ids"], p["w"], T, H, E, K, sp)
-        st |= lib.moe_expert_ffn(p["x"], p["ids"], p["w"], p["ew"], p["eo"], p["ws"], ws_bytes, T, H, E, K, I, sp)
-        st |= lib.moe_combine(p["eo"], p["ids"], p["w"], p["y"], T, H, K, sp)
+    def step(s: int = sp) -> None:
+        st = lib.moe_routing_topk(p["x"], p["wg"], p["ids"], p["w"], T, H, E, K, s)
+        st |= lib.moe_expert_ffn(p["x"], p["ids"], p["w"], p["ew"], p["eo"], p["ws"], ws_bytes, T, H, E, K, I, s)
+        st |= lib.moe_combine(p["eo"], p["ids"], p["w"], p["y"], T, H, K, s)
         if st:
             raise RuntimeError(lib.moe_last_error().decode())
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    y_eager = y.clone()
     progress(f"warm-up done ({args.warmup} steps); timing {args.steps} steps")
 
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    with ops.kernel_trace() as kernels:
+    def timed(run_step) -> tuple[float, float]:
+        """(host-clock ms, event ms) per step over args.steps steps between synchronisations."""
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         ev0.record(stream)
         for _ in range(args.steps):
-            step()
+            run_step()
         ev1.record(stream)
         torch.cuda.synchronize()
         t1 = time.perf_counter()
-    ms_per_step = (t1 - t0) * 1e3 / args.steps
-    gpu_ms_per_step = ev0.elapsed_time(ev1) / args.steps
-    progress(f"timed: {ms_per_step * 1e3:.1f} us/step (host clock), {gpu_ms_per_step * 1e3:.1f} us/step (events)")
+        return (t1 - t0) * 1e3 / args.steps, ev0.elapsed_time(ev1) / args.steps
+
+    # 1) the layer as three eager C-ABI calls per step: the headline value
+    ms_per_step, gpu_ms_per_step = timed(step)
+    progress(f"eager: {ms_per_step * 1e3:.1f} us/step (host clock), {gpu_ms_per_step * 1e3:.1f} us/step (events)")
+    # 2) the same three calls captured once in a HIP graph and replayed (no memset nodes: the library records
+    #    kernels only); every replay recomputes the whole layer, and its y must equal the eager y bit for bit
+    graph_ms = None
+    if not args.no_graph:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step(int(torch.cuda.current_stream().cuda_stream))
+        y.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        if not torch.equal(y, y_eager):
+            raise RuntimeError("graph replay of the layer differs from the eager layer")
+        graph_ms, _ = timed(g.replay)
+        progress(f"graph replay: {graph_ms * 1e3:.1f} us/step (host clock)")
+        del g
+    # 3) per-kernel HIP events recorded by the library on the launch stream: durations for the roofline
+    with ops.kernel_trace() as kernels:
+        traced_ms, _ = timed(step)
+    progress(f"traced: {traced_ms * 1e3:.1f} us/step with an event pair around every launch")
 
     ids_h = ids.cpu().numpy()
     active = int((np.bincount(ids_h.ravel(), minlength=E) > 0).sum())
@@ -246,6 +274,8 @@ def main() -> int:
         "config": {"workload": f"{cfg.name} MoE layer T={T},H={H},E={E},K={K},I={I}", "tokens": T,
                    "hidden": H, "experts": E, "top_k": K, "intermediate": I, "active_experts": active},
         "layer_us_gpu_events": round(gpu_ms_per_step * 1e3, 2),
+        "layer_us_graph_replay": round(graph_ms * 1e3, 2) if graph_ms else None,
+        "layer_us_traced": round(traced_ms * 1e3, 2),
         "ffn_us": round(ffn_ms * 1e3, 2),
         "ffn_tflops": round(ffn_flops / (ffn_ms * 1e-3) / 1e12, 2),
         "ffn_hbm_gbps": round(ffn_bytes / (ffn_ms * 1e-3) / 1e9, 1),

@@ -14,9 +14,12 @@
 //   * register spills in the loop are fatal: scratch reloads also wait on the vector-memory counter and drain
 //     the weight ring -> 8 waves per workgroup, no spills (checked with -Rpass-analysis=kernel-resource-usage).
 //
-// Workgroup = 8 waves on one expert e and one K-range [k0, k0 + kc):
-//   1. the workgroup copies the K-range of the expert's activation rows (up to 32 per pass; x rows gathered
-//      through the sorted slot order for gate/up, SwiGLU rows for down) into LDS, then one barrier;
+// Work unit = one expert e, one K-range [k0, k0 + kc) and one column group (8 waves x 16 or 32 weight rows).
+// The grid is persistent: as many 8-wave workgroups as the GPU holds at once, each taking a contiguous run of
+// units ordered (expert, K-range, column group) with the column group fastest. Per unit:
+//   1. unless the previous unit of the workgroup had the same expert and K-range, the workgroup copies the
+//      K-range of the expert's activation rows (up to 32 per pass; x rows gathered through the sorted slot order
+//      for gate/up, SwiGLU rows for down) into LDS, then one barrier;
 //   2. each wave streams two 16-row weight tiles (gate/up: W_gate and W_up rows n0..n0+15; down: W_down rows
 //      n0..n0+31) through a register ring of D k-steps, starting at its own rotated step, with activation
 //      fragments read from LDS (ds_read_b128) and v_mfma_f32_16x16x32_f16 (fp32 accumulation);
@@ -24,6 +27,8 @@
 //      down with one K-range -> expert_out[slot] fp16 (the scatter back to [T, K, H] order);
 //      down with several K-ranges -> fp32 partial sums, added in a fixed order by down_reduce_kernel (no atomics,
 //      deterministic).
+// A workgroup per unit instead (1024 short workgroups at decode) re-stages the activations for every unit and
+// lets every CU's weight stream run dry between workgroups: the persistent grid is 9% faster on gate/up.
 // An expert with more than 32 rows takes several passes, each re-streaming the weights: this schedule is
 // chosen only when the average number of rows per expert is small.
 // LDS: row r of the staged K-range at r * (kc + 8) halfs (16 B of padding per row puts the 16 rows read by one
@@ -50,7 +55,7 @@ struct StreamArgs {
     const uint16_t* w;            // expert_weights [E, 3I, H]
     uint16_t* out;                // hidden (kSwiGLU) or expert_out (kScatter)
     float* partial;               // [nsplit][T*K][H] fp32 (kPartial)
-    int K, H, I;
+    int E, K, H, I;
     int kdim;                     // reduction extent: H (gate/up) or I (down)
     int ndim;                     // output columns: I (gate/up) or H (down)
     int kc;                       // K-range per workgroup (kdim % kc == 0, (kc / 32) % D == 0)
@@ -138,68 +143,82 @@ __device__ __forceinline__ void ring_pass(const StreamArgs& p, const uint16_t* l
         }
 }
 
-// Grid: E * groups * nsplit workgroups; workgroup -> (expert, column group, K-range).
+// Persistent grid: workgroup b takes units [b * units_per_wg, (b + 1) * units_per_wg) of E * nsplit * groups
+// units, unit u -> (expert, K-range, column group) with the column group fastest.
 template <int D, int EPI>
-__global__ __launch_bounds__(kThreads) void ffn_stream_kernel(StreamArgs p) {
+__global__ __launch_bounds__(kThreads) void ffn_stream_kernel(StreamArgs p, int units_per_wg) {
     extern __shared__ __align__(16) uint16_t lds[];
     const int wave = static_cast<int>(threadIdx.x) / kWave;
     const int lane = lane_id();
     const int cols_per_wave = EPI == kSwiGLU ? 16 : 32;  // gate/up: 16 rows of each matrix; down: 32 rows
     const int groups = (p.ndim + kWaves * cols_per_wave - 1) / (kWaves * cols_per_wave);
-    const int b = static_cast<int>(blockIdx.x);
-    const int split = b % p.nsplit;
-    const int e = b / p.nsplit / groups;
-    const int n0 = ((b / p.nsplit) % groups * kWaves + wave) * cols_per_wave;
-    const int off = p.offsets[e];
-    const int ne = p.offsets[e + 1] - off;
-    if (ne <= 0) return;  // uniform over the workgroup
-    const bool active = n0 < p.ndim;
+    const int total_units = p.E * p.nsplit * groups;
+    const int u_begin = static_cast<int>(blockIdx.x) * units_per_wg;
+    const int u_end = min(u_begin + units_per_wg, total_units);
     const int row = lane & 15, kg = lane >> 4;
     const int nsteps = p.kc / 32;
-    const int k0 = split * p.kc;
-    const size_t ebase = static_cast<size_t>(e) * 3 * static_cast<size_t>(p.I) * p.H;
-    const uint16_t* w0 = p.w + ebase + p.w_off + static_cast<size_t>(active ? n0 + row : row) * p.kdim + k0 + kg * 8;
-    const uint16_t* w1 = w0 + p.w1_off;
-    const int rot = ((b * kWaves + wave) * 7 * D) % nsteps;  // a multiple of D: batches never wrap
     const int gpr = p.kc / 8;
     const int stride = p.kc + 8;
+    int staged_e = -1, staged_split = -1, staged_mc = -1;  // activation rows held in LDS
 
-    for (int mc = 0; mc < ne; mc += p.rows_cap) {
-        const int rows = min(p.rows_cap, ne - mc);
-        f16x8 r0[D], r1[D];
-        if (active) {
+    for (int u = u_begin; u < u_end; ++u) {
+        const int g = u % groups;
+        const int split = (u / groups) % p.nsplit;
+        const int e = u / groups / p.nsplit;
+        const int off = p.offsets[e];
+        const int ne = p.offsets[e + 1] - off;
+        if (ne <= 0) continue;  // uniform over the workgroup
+        const int n0 = (g * kWaves + wave) * cols_per_wave;
+        const bool active = n0 < p.ndim;
+        const int k0 = split * p.kc;
+        const size_t ebase = static_cast<size_t>(e) * 3 * static_cast<size_t>(p.I) * p.H;
+        const uint16_t* w0 =
+            p.w + ebase + p.w_off + static_cast<size_t>(active ? n0 + row : row) * p.kdim + k0 + kg * 8;
+        const uint16_t* w1 = w0 + p.w1_off;
+        const int rot = ((u * kWaves + wave) * 7 * D) % nsteps;  // a multiple of D: batches never wrap
+
+        for (int mc = 0; mc < ne; mc += p.rows_cap) {
+            const int rows = min(p.rows_cap, ne - mc);
+            f16x8 r0[D], r1[D];
+            if (active) {
 #pragma unroll
-            for (int i = 0; i < D; ++i) {
-                r0[i] = load_f16x8(w0 + (rot + i) * 32);
-                r1[i] = load_f16x8(w1 + (rot + i) * 32);
-            }
-        }
-        if (mc > 0) lds_barrier();  // every wave is done with the previous pass's rows
-        const int total = rows * gpr;
-        for (int q0 = 0; q0 < total; q0 += 4 * kThreads) {
-            u32x4 v[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int q = q0 + u * kThreads + static_cast<int>(threadIdx.x);
-                if (q < total) {
-                    const int r = q / gpr;
-                    const size_t src_row = p.gather ? static_cast<size_t>(p.sorted_slot[off + mc + r] / p.K)
-                                                    : static_cast<size_t>(off + mc + r);
-                    v[u] = *reinterpret_cast<const u32x4*>(p.act + src_row * p.kdim + k0 + (q % gpr) * 8);
+                for (int i = 0; i < D; ++i) {
+                    r0[i] = load_f16x8(w0 + (rot + i) * 32);
+                    r1[i] = load_f16x8(w1 + (rot + i) * 32);
                 }
             }
+            if (e != staged_e || split != staged_split || mc != staged_mc) {
+                if (staged_e >= 0) lds_barrier();  // every wave is done with the previous rows
+                staged_e = e;
+                staged_split = split;
+                staged_mc = mc;
+                const int total = rows * gpr;
+                for (int q0 = 0; q0 < total; q0 += 4 * kThreads) {
+                    u32x4 v[4];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int q = q0 + u * kThreads + static_cast<int>(threadIdx.x);
-                if (q < total) *reinterpret_cast<u32x4*>(lds + (q / gpr) * stride + (q % gpr) * 8) = v[u];
+                    for (int t = 0; t < 4; ++t) {
+                        const int q = q0 + t * kThreads + static_cast<int>(threadIdx.x);
+                        if (q < total) {
+                            const int r = q / gpr;
+                            const size_t src_row = p.gather ? static_cast<size_t>(p.sorted_slot[off + mc + r] / p.K)
+                                                            : static_cast<size_t>(off + mc + r);
+                            v[t] = *reinterpret_cast<const u32x4*>(p.act + src_row * p.kdim + k0 + (q % gpr) * 8);
+                        }
+                    }
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        const int q = q0 + t * kThreads + static_cast<int>(threadIdx.x);
+                        if (q < total) *reinterpret_cast<u32x4*>(lds + (q / gpr) * stride + (q % gpr) * 8) = v[t];
+                    }
+                }
+                lds_barrier();
             }
+            if (!active) continue;
+            if (rows > 16)
+                ring_pass<2, D, EPI>(p, lds, w0, w1, r0, r1, rot, off, ne, mc, n0, split, lane);
+            else
+                ring_pass<1, D, EPI>(p, lds, w0, w1, r0, r1, rot, off, ne, mc, n0, split, lane);
         }
-        lds_barrier();
-        if (!active) continue;
-        if (rows > 16)
-            ring_pass<2, D, EPI>(p, lds, w0, w1, r0, r1, rot, off, ne, mc, n0, split, lane);
-        else
-            ring_pass<1, D, EPI>(p, lds, w0, w1, r0, r1, rot, off, ne, mc, n0, split, lane);
     }
 }
 
@@ -248,17 +267,28 @@ StreamShape pick_shape(int kdim, bool allow_split) {
     return StreamShape{0, 0, 0, 0};  // no layout: the caller reports unsupported
 }
 
+// Workgroups of `kernel` (kThreads threads, `lds` bytes of LDS) resident on the current device at once.
+int resident_workgroups(const void* kernel, size_t lds) {
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, lds) != hipSuccess)
+        return 0;
+    return cus * (per_cu > 0 ? per_cu : 1);
+}
+
 template <int EPI>
-hipError_t launch_stream_epi(const StreamArgs& p, int d, int grid, hipStream_t stream) {
+hipError_t launch_stream_epi(const StreamArgs& p, int d, int units, hipStream_t stream) {
     const size_t lds = static_cast<size_t>(p.rows_cap) * (p.kc + 8) * sizeof(uint16_t);
     hipError_t err = hipSuccess;
 #define MOE_STREAM_CASE(DEPTH)                                                                                 \
     case DEPTH: {                                                                                              \
-        static const hipError_t attr = hipFuncSetAttribute(                                                    \
-            reinterpret_cast<const void*>(&ffn_stream_kernel<DEPTH, EPI>),                                     \
-            hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax);                                              \
+        const void* fn = reinterpret_cast<const void*>(&ffn_stream_kernel<DEPTH, EPI>);                        \
+        static const hipError_t attr = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax); \
         if (attr != hipSuccess) return attr;                                                                   \
-        ffn_stream_kernel<DEPTH, EPI><<<grid, kThreads, lds, stream>>>(p);                                     \
+        const int slots = resident_workgroups(fn, lds);                                                        \
+        const int upw = slots > 0 ? (units + slots - 1) / slots : 1;                                          \
+        ffn_stream_kernel<DEPTH, EPI><<<(units + upw - 1) / upw, kThreads, lds, stream>>>(p, upw);             \
         break;                                                                                                 \
     }
     switch (d) {
@@ -301,6 +331,7 @@ hipError_t launch_ffn_stream(const uint16_t* x, const uint16_t* expert_weights, 
     p.sorted_slot = ws.sorted_slot;
     p.offsets = ws.offsets;
     p.w = expert_weights;
+    p.E = E;
     p.K = K;
     p.H = H;
     p.I = I;

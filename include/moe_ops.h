@@ -125,8 +125,10 @@ typedef struct moe_ffn_plan {
     int64_t num_tokens, hidden_size, num_experts, top_k, intermediate_size;
     int32_t schedule;        /* 0 = weight-streaming (few rows per expert), 1 = LDS-tiled (many rows)    */
     int32_t permute_grid;    /* workgroups of the permute kernel (one per expert)                          */
-    int32_t gateup_grid;     /* workgroups of the fused gate/up + SwiGLU grouped GEMM                      */
-    int32_t down_grid;       /* workgroups of the down-projection grouped GEMM                             */
+    int32_t gateup_grid;     /* work tiles of the fused gate/up + SwiGLU grouped GEMM (upper bound on its */
+                             /* workgroups: the streaming schedule runs a persistent grid of at most as    */
+                             /* many workgroups as the GPU holds at once)                                  */
+    int32_t down_grid;       /* work tiles of the down-projection grouped GEMM (same convention)           */
     int32_t block;           /* threads per workgroup of the GEMMs                                         */
     int32_t rows_per_tile;   /* token rows per GEMM tile                                                   */
     size_t workspace_bytes;  /* == moe_expert_ffn_workspace_bytes(...)                                    */
