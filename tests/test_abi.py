@@ -95,7 +95,9 @@ def test_combine_infer_shape(lib):
 def test_plans(lib):
     rp = lib_mod.RoutingPlan()
     assert lib.moe_routing_topk_plan(128, 2048, 16, 2, C.byref(rp)) == MOE_OK
-    assert (rp.grid, rp.block, rp.tokens_per_block, rp.workspace_bytes) == (8, 256, 16, 0)
+    assert (rp.grid, rp.block, rp.tokens_per_block, rp.workspace_bytes) == (8, 1024, 16, 0)
+    assert rp.lds_bytes == 16 * 16 * 16 * 4  # 16 waves x 16 tokens x 16 experts of fp32 partials
+    assert lib.moe_routing_topk_plan(128, 2048, 256, 8, C.byref(rp)) == MOE_OK and rp.block == 256
     assert lib.moe_routing_topk_plan(128, 2040, 16, 2, C.byref(rp)) == ERR_UNSUP
     assert lib.moe_routing_topk_plan(128, 2048, 300, 2, C.byref(rp)) == ERR_UNSUP
     fp = lib_mod.FfnPlan()
