@@ -21,6 +21,7 @@ namespace {
 
 constexpr int kCombineThreads = 256;
 constexpr int kElems = 8;
+constexpr int kBatch = 8;
 
 __global__ __launch_bounds__(kCombineThreads) void combine_kernel(const uint16_t* __restrict__ expert_out,
                                                                   const uint16_t* __restrict__ weights,
@@ -35,11 +36,24 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(const uint16_t
     for (int j = 0; j < kElems; ++j) acc[j] = 0.0f;
     const uint16_t* wrow = weights + static_cast<size_t>(t) * K;
     const uint16_t* orow = expert_out + static_cast<size_t>(t) * K * H + c;
-    for (int k = 0; k < K; ++k) {
-        const float w = f16_bits_to_f32(wrow[k]);
-        const f16x8 o = load_f16x8(orow + static_cast<size_t>(k) * H);
+    // up to kBatch rows are loaded before they are accumulated (still in ascending k)
+    for (int k0 = 0; k0 < K; k0 += kBatch) {
+        f16x8 o[kBatch];
+        float w[kBatch];
 #pragma unroll
-        for (int j = 0; j < kElems; ++j) acc[j] = acc[j] + w * static_cast<float>(o[j]);
+        for (int u = 0; u < kBatch; ++u) {
+            if (k0 + u < K) {
+                w[u] = f16_bits_to_f32(wrow[k0 + u]);
+                o[u] = load_f16x8(orow + static_cast<size_t>(k0 + u) * H);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            if (k0 + u < K) {
+#pragma unroll
+                for (int j = 0; j < kElems; ++j) acc[j] = acc[j] + w[u] * static_cast<float>(o[u][j]);
+            }
+        }
     }
     f16x8 out;
 #pragma unroll

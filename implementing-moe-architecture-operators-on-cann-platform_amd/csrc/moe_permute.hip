@@ -19,6 +19,7 @@ namespace moe {
 namespace {
 
 constexpr int kPermuteWaves = 16;
+constexpr int kUnroll = 8;
 
 __global__ __launch_bounds__(kPermuteWaves * kWave) void permute_kernel(const int32_t* __restrict__ ids, int S, int E,
                                                                           int H, int32_t* __restrict__ offsets,
@@ -33,12 +34,20 @@ __global__ __launch_bounds__(kPermuteWaves * kWave) void permute_kernel(const in
     const int beg = min(S, wave * chunk);
     const int end = min(S, beg + chunk);
 
+    // kUnroll loads per lane are issued before their ballots: the chunk is read in a few round trips
     int n_eq = 0, n_lt = 0;
-    for (int base = beg; base < end; base += kWave) {
-        const int s = base + lane;
-        const int id = s < end ? ids[s] : -1;
-        n_eq += __popcll(__ballot(id == e));
-        n_lt += __popcll(__ballot(id >= 0 && id < e));
+    for (int base = beg; base < end; base += kUnroll * kWave) {
+        int id[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const int s = base + u * kWave + lane;
+            id[u] = s < end ? ids[s] : -1;
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            n_eq += __popcll(__ballot(id[u] == e));
+            n_lt += __popcll(__ballot(id[u] >= 0 && id[u] < e));
+        }
     }
     if (lane == 0) {
         cnt_eq[wave] = n_eq;
@@ -59,12 +68,19 @@ __global__ __launch_bounds__(kPermuteWaves * kWave) void permute_kernel(const in
 
     const uint64_t below = (uint64_t{1} << lane) - 1;
     int pos = off + before;
-    for (int base = beg; base < end; base += kWave) {
-        const int s = base + lane;
-        const int id = s < end ? ids[s] : -1;
-        const uint64_t m = __ballot(id == e);
-        if (id == e) sorted_slot[pos + __popcll(m & below)] = s;
-        pos += __popcll(m);
+    for (int base = beg; base < end; base += kUnroll * kWave) {
+        int id[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const int s = base + u * kWave + lane;
+            id[u] = s < end ? ids[s] : -1;
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const uint64_t m = __ballot(id[u] == e);
+            if (id[u] == e) sorted_slot[pos + __popcll(m & below)] = base + u * kWave + lane;
+            pos += __popcll(m);
+        }
     }
 
     if (e != 0) return;

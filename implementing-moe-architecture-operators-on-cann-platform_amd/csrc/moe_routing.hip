@@ -13,7 +13,7 @@
 //   Phase 2: one lane per token runs softmax, top-K and renormalisation sequentially over the experts, in the
 //            oracle's order of operations: max scan from -1e30, expf(l - max), ascending-expert sum, division by
 //            the sum; K rounds of a strict '>' scan (lowest index wins an exact tie); wSum over the K picks in
-//            rank order; p / wSum; fp16 round-to-nearest-even. For E <= 32 the lane holds its row in registers
+//            rank order; p / wSum; fp16 round-to-nearest-even. For E <= 64 the lane holds its row in registers
 //            (16-byte LDS reads), otherwise it works on its LDS row.
 // HBM traffic per launch: T*H*2 (x) + H*E*2 (w_gate, L2-resident after the first workgroups) + T*K*6 bytes.
 
@@ -27,7 +27,8 @@ namespace {
 constexpr int kTokensPerBlock = 16;
 
 constexpr int waves_for(int eb) { return eb <= 2 ? 16 : 4; }
-constexpr int unroll_for(int eb) { return eb == 1 ? 4 : eb == 2 ? 2 : 1; }  // 1024 threads: 128 VGPRs
+// k-steps whose loads are issued together: E <= 32 runs 1024 threads (128 VGPRs per lane), larger E 256
+constexpr int unroll_for(int eb) { return eb == 1 ? 4 : eb == 2 ? 2 : eb == 4 ? 4 : 2; }
 
 // softmax + top-K + renormalisation of one token's logits L[0..E) held in registers (Epad = EB * 16 >= E)
 template <int Epad>
@@ -175,7 +176,7 @@ __global__ __launch_bounds__(waves_for(EB) * kWave) void routing_topk_kernel(con
     if (t0 + t >= T) return;
     int32_t* ids_out = expert_ids + static_cast<size_t>(t0 + t) * K;
     uint16_t* w_out = weights + static_cast<size_t>(t0 + t) * K;
-    if constexpr (EB <= 2) {
+    if constexpr (EB <= 4) {
         float L[Epad];
 #pragma unroll
         for (int e = 0; e < Epad; e += 4) {
