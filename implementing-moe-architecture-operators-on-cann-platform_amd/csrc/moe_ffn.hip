@@ -1,8 +1,9 @@
 // moe_ffn.hip -- MoeExpertFFN: workspace layout and schedule dispatch of the grouped GEMMs.
 //
 // Reference: op_kernel/moe_expert_ffn.cpp:613-621 (kernel entry), op_host/moe_ops.cpp:340-349 (workspace).
-// The expert FFN runs as three kernels on one stream:
-//   moe_permute.hip      expert-sorted slot order + per-expert offsets (workspace)
+// The expert FFN runs on one stream as
+//   permute              expert-sorted slot order + per-expert offsets (workspace): moe_permute.hip for the
+//                        tiled schedule; the streaming gate/up kernel finds its rows itself
 //   gate/up + SwiGLU     hidden[r, :] = silu(x_t W_gate_e^T) * (x_t W_up_e^T) for sorted row r = (t, k), fp16
 //   down + scatter       expert_out[t, k, :] = hidden[r, :] W_down_e^T, fp16
 // The grouped GEMMs have two schedules, chosen on the host from the average number of rows per expert
@@ -33,7 +34,7 @@ int ffn_schedule(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
 }
 
 // Layout (each region 256-byte aligned): offsets [E+1] i32 | sorted_slot [T*K] i32 | hidden [T*K, I] fp16 |
-// partial [nsplit, T*K, H] fp32 (only when the down projection is split over K).
+// partial [nsplit, T*K, H] fp32 (weight-streaming schedule, when the down projection is split over K).
 size_t ffn_workspace_bytes(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
     const size_t S = static_cast<size_t>(T) * static_cast<size_t>(K);
     size_t bytes = align_up(sizeof(int32_t) * static_cast<size_t>(E + 1), 256);
@@ -77,11 +78,15 @@ FfnGrid ffn_grid(int T, int H, int E, int K, int I) {
     return g;
 }
 
-hipError_t launch_ffn(const uint16_t* x, const uint16_t* expert_weights, uint16_t* expert_out, FfnWorkspace ws,
-                      int T, int H, int E, int K, int I, hipStream_t stream) {
+hipError_t launch_ffn(const uint16_t* x, const int32_t* expert_ids, const uint16_t* expert_weights,
+                      uint16_t* expert_out, FfnWorkspace ws, int T, int H, int E, int K, int I, hipStream_t stream) {
     switch (ffn_schedule(T, H, E, K, I)) {
-        case 1: return launch_ffn_tiled(x, expert_weights, expert_out, ws, T, H, E, K, I, stream);
-        case 0: return launch_ffn_stream(x, expert_weights, expert_out, ws, T, H, E, K, I, stream);
+        case 1: {
+            const hipError_t err = launch_permute(expert_ids, T * K, E, H, ws, expert_out, stream);
+            if (err != hipSuccess) return err;
+            return launch_ffn_tiled(x, expert_weights, expert_out, ws, T, H, E, K, I, stream);
+        }
+        case 0: return launch_ffn_stream(x, expert_ids, expert_weights, expert_out, ws, T, H, E, K, I, stream);
         default: return hipErrorInvalidValue;
     }
 }

@@ -17,16 +17,22 @@
 // Work unit = one expert e, one K-range [k0, k0 + kc) and one column group (8 waves x 16 or 32 weight rows).
 // The grid is persistent: as many 8-wave workgroups as the GPU holds at once, each taking a contiguous run of
 // units ordered (expert, K-range, column group) with the column group fastest. Per unit:
-//   1. unless the previous unit of the workgroup had the same expert and K-range, the workgroup copies the
-//      K-range of the expert's activation rows (up to 32 per pass; x rows gathered through the sorted slot order
-//      for gate/up, SwiGLU rows for down) into LDS, then one barrier;
-//   2. each wave streams two 16-row weight tiles (gate/up: W_gate and W_up rows n0..n0+15; down: W_down rows
+//   1. gate/up finds the expert's rows itself: two ballot scans of expert_ids (count, then rank) give the
+//      expert's first sorted row and the slots of the current pass, so no separate permute kernel runs; the
+//      workgroup holding the expert's first column group also writes offsets[e] and the expert's sorted_slot
+//      entries for the down kernel. Down reads them.
+//   2. unless the previous unit of the workgroup had the same expert, K-range and pass, the workgroup copies
+//      the K-range of the pass's activation rows (up to 32; x rows gathered by slot / K for gate/up, SwiGLU rows
+//      for down) into LDS, then one barrier;
+//   3. each wave streams two 16-row weight tiles (gate/up: W_gate and W_up rows n0..n0+15; down: W_down rows
 //      n0..n0+31) through a register ring of D k-steps, starting at its own rotated step, with activation
 //      fragments read from LDS (ds_read_b128) and v_mfma_f32_16x16x32_f16 (fp32 accumulation);
-//   3. epilogue in registers: gate/up -> hidden = silu(gate) * up (fp32) -> fp16 workspace row;
+//   4. epilogue in registers: gate/up -> hidden = silu(gate) * up (fp32) -> fp16 workspace row;
 //      down with one K-range -> expert_out[slot] fp16 (the scatter back to [T, K, H] order);
 //      down with several K-ranges -> fp32 partial sums, added in a fixed order by down_reduce_kernel (no atomics,
-//      deterministic).
+//      deterministic). Letting the last of the nsplit workgroups of an (expert, column group) add them instead
+//      (a device-scope arrival counter, partials written and read with device-scope accesses) was measured
+//      slower at decode: 121.6 us for down against 104 + 6.5 us for down + reduce.
 // A workgroup per unit instead (1024 short workgroups at decode) re-stages the activations for every unit and
 // lets every CU's weight stream run dry between workgroups: the persistent grid is 9% faster on gate/up.
 // An expert with more than 32 rows takes several passes, each re-streaming the weights: this schedule is
@@ -44,7 +50,7 @@ namespace {
 constexpr int kWaves = 8;                 // streaming waves per workgroup
 constexpr int kThreads = kWaves * kWave;  // 512
 constexpr int kMaxRows = 32;              // activation rows per pass (two 16-row MFMA tiles)
-constexpr int kLdsMax = 160 * 1024;       // gfx950 LDS per workgroup
+constexpr int kLdsMax = 160 * 1024 - 1024;  // gfx950 LDS per workgroup, less 1 KB for the static arrays
 
 enum Epilogue { kSwiGLU = 0, kScatter = 1, kPartial = 2 };
 
@@ -65,6 +71,11 @@ struct StreamArgs {
     size_t w_off;                 // first weight matrix inside an expert block: 0 (gate) or 2*I*H (down)
     size_t w1_off;                // second weight tile relative to the first: I*H (up) or 16*I (next 16 rows)
     int gather;                   // activation row r is x[sorted_slot[r] / K] (gate/up) or hidden[r] (down)
+    const int32_t* ids;           // expert_ids [T*K]: gate/up finds each expert's rows by scanning them
+    int S;                        // T*K
+    int32_t* offsets_out;         // gate/up writes offsets [E+1] and sorted_slot [T*K] for the down kernel
+    int32_t* sorted_out;
+    uint16_t* expert_out;         // gate/up zeroes the rows of ids outside [0, E)
 };
 
 __device__ __forceinline__ void lds_barrier() {
@@ -143,13 +154,72 @@ __device__ __forceinline__ void ring_pass(const StreamArgs& p, const uint16_t* l
         }
 }
 
+// Expert e's rows by scanning ids: wave w takes the contiguous chunk w of the T*K slots.
+// count: per-wave numbers of ids == e and of valid ids < e into s_eq / s_lt (the caller then barriers);
+// rank:  the slots of e in ascending order get ranks 0..ne-1; those in [mc, mc + cap) go to s_rows, and with
+//        `sorted` non-null every slot is written to sorted[off + rank].
+__device__ __forceinline__ void expert_count(const StreamArgs& p, int e, int* s_eq, int* s_lt) {
+    const int wave = static_cast<int>(threadIdx.x) / kWave, lane = lane_id();
+    const int chunk = ((p.S + kWaves - 1) / kWaves + kWave - 1) / kWave * kWave;
+    const int beg = min(p.S, wave * chunk), end = min(p.S, beg + chunk);
+    int n_eq = 0, n_lt = 0;
+    for (int base = beg; base < end; base += 4 * kWave) {
+        int id[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int sl = base + u * kWave + lane;
+            id[u] = sl < end ? p.ids[sl] : -1;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            n_eq += __popcll(__ballot(id[u] == e));
+            n_lt += __popcll(__ballot(id[u] >= 0 && id[u] < e));
+        }
+    }
+    if (lane == 0) {
+        s_eq[wave] = n_eq;
+        s_lt[wave] = n_lt;
+    }
+}
+
+__device__ __forceinline__ void expert_rank(const StreamArgs& p, int e, int before, int off, int mc, int cap,
+                                            int* s_rows, int32_t* sorted) {
+    const int wave = static_cast<int>(threadIdx.x) / kWave, lane = lane_id();
+    const int chunk = ((p.S + kWaves - 1) / kWaves + kWave - 1) / kWave * kWave;
+    const int beg = min(p.S, wave * chunk), end = min(p.S, beg + chunk);
+    const uint64_t below = (uint64_t{1} << lane) - 1;
+    int pos = before;
+    for (int base = beg; base < end; base += 4 * kWave) {
+        int id[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int sl = base + u * kWave + lane;
+            id[u] = sl < end ? p.ids[sl] : -1;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint64_t m = __ballot(id[u] == e);
+            if (id[u] == e) {
+                const int rank = pos + __popcll(m & below);
+                const int sl = base + u * kWave + lane;
+                if (rank >= mc && rank < mc + cap) s_rows[rank - mc] = sl;
+                if (sorted) sorted[off + rank] = sl;
+            }
+            pos += __popcll(m);
+        }
+    }
+}
+
 // Persistent grid: workgroup b takes units [b * units_per_wg, (b + 1) * units_per_wg) of E * nsplit * groups
 // units, unit u -> (expert, K-range, column group) with the column group fastest.
 template <int D, int EPI>
 __global__ __launch_bounds__(kThreads) void ffn_stream_kernel(StreamArgs p, int units_per_wg) {
     extern __shared__ __align__(16) uint16_t lds[];
+    __shared__ int s_eq[kWaves], s_lt[kWaves];
+    __shared__ int s_rows[kMaxRows];
     const int wave = static_cast<int>(threadIdx.x) / kWave;
     const int lane = lane_id();
+    const int tid = static_cast<int>(threadIdx.x);
     const int cols_per_wave = EPI == kSwiGLU ? 16 : 32;  // gate/up: 16 rows of each matrix; down: 32 rows
     const int groups = (p.ndim + kWaves * cols_per_wave - 1) / (kWaves * cols_per_wave);
     const int total_units = p.E * p.nsplit * groups;
@@ -159,14 +229,48 @@ __global__ __launch_bounds__(kThreads) void ffn_stream_kernel(StreamArgs p, int 
     const int nsteps = p.kc / 32;
     const int gpr = p.kc / 8;
     const int stride = p.kc + 8;
-    int staged_e = -1, staged_split = -1, staged_mc = -1;  // activation rows held in LDS
 
+    if (EPI == kSwiGLU && blockIdx.x == 0) {
+        // once per call: zero the expert_out rows of invalid ids (they belong to no expert)
+        for (int sl = tid; sl < p.S; sl += kThreads) {
+            const int id = p.ids[sl];
+            if (id >= 0 && id < p.E) continue;
+            u32x4* dst = reinterpret_cast<u32x4*>(p.expert_out + static_cast<size_t>(sl) * p.H);
+            for (int j = 0; j < p.H / 8; ++j) dst[j] = u32x4{0u, 0u, 0u, 0u};
+        }
+    }
+
+    int cur_e = -1, off = 0, ne = 0, before = 0;          // expert whose counts are known (gate/up)
+    int staged_e = -1, staged_split = -1, staged_mc = -1;  // activation rows held in LDS
     for (int u = u_begin; u < u_end; ++u) {
         const int g = u % groups;
         const int split = (u / groups) % p.nsplit;
         const int e = u / groups / p.nsplit;
-        const int off = p.offsets[e];
-        const int ne = p.offsets[e + 1] - off;
+        if (EPI == kSwiGLU) {
+            if (e != cur_e) {
+                if (cur_e >= 0) lds_barrier();  // every wave is done with the previous expert's counts and rows
+                expert_count(p, e, s_eq, s_lt);
+                lds_barrier();
+                off = 0;
+                ne = 0;
+                before = 0;
+#pragma unroll
+                for (int w = 0; w < kWaves; ++w) {
+                    off += s_lt[w];
+                    ne += s_eq[w];
+                    if (w < wave) before += s_eq[w];
+                }
+                cur_e = e;
+                staged_mc = -1;
+                if (g == 0 && tid == 0) {
+                    p.offsets_out[e] = off;
+                    if (e == p.E - 1) p.offsets_out[p.E] = off + ne;
+                }
+            }
+        } else {
+            off = p.offsets[e];
+            ne = p.offsets[e + 1] - off;
+        }
         if (ne <= 0) continue;  // uniform over the workgroup
         const int n0 = (g * kWaves + wave) * cols_per_wave;
         const bool active = n0 < p.ndim;
@@ -192,33 +296,40 @@ __global__ __launch_bounds__(kThreads) void ffn_stream_kernel(StreamArgs p, int 
                 staged_e = e;
                 staged_split = split;
                 staged_mc = mc;
+                if (EPI == kSwiGLU) {
+                    expert_rank(p, e, before, off, mc, p.rows_cap, s_rows,
+                                g == 0 && mc == 0 ? p.sorted_out : nullptr);
+                    lds_barrier();
+                }
                 const int total = rows * gpr;
                 for (int q0 = 0; q0 < total; q0 += 4 * kThreads) {
                     u32x4 v[4];
 #pragma unroll
                     for (int t = 0; t < 4; ++t) {
-                        const int q = q0 + t * kThreads + static_cast<int>(threadIdx.x);
+                        const int q = q0 + t * kThreads + tid;
                         if (q < total) {
                             const int r = q / gpr;
-                            const size_t src_row = p.gather ? static_cast<size_t>(p.sorted_slot[off + mc + r] / p.K)
+                            const size_t src_row = p.gather ? static_cast<size_t>(s_rows[r] / p.K)
                                                             : static_cast<size_t>(off + mc + r);
                             v[t] = *reinterpret_cast<const u32x4*>(p.act + src_row * p.kdim + k0 + (q % gpr) * 8);
                         }
                     }
 #pragma unroll
                     for (int t = 0; t < 4; ++t) {
-                        const int q = q0 + t * kThreads + static_cast<int>(threadIdx.x);
+                        const int q = q0 + t * kThreads + tid;
                         if (q < total) *reinterpret_cast<u32x4*>(lds + (q / gpr) * stride + (q % gpr) * 8) = v[t];
                     }
                 }
                 lds_barrier();
             }
-            if (!active) continue;
-            if (rows > 16)
-                ring_pass<2, D, EPI>(p, lds, w0, w1, r0, r1, rot, off, ne, mc, n0, split, lane);
-            else
-                ring_pass<1, D, EPI>(p, lds, w0, w1, r0, r1, rot, off, ne, mc, n0, split, lane);
+            if (active) {
+                if (rows > 16)
+                    ring_pass<2, D, EPI>(p, lds, w0, w1, r0, r1, rot, off, ne, mc, n0, split, lane);
+                else
+                    ring_pass<1, D, EPI>(p, lds, w0, w1, r0, r1, rot, off, ne, mc, n0, split, lane);
+            }
         }
+
     }
 }
 
@@ -285,7 +396,10 @@ hipError_t launch_stream_epi(const StreamArgs& p, int d, int units, hipStream_t 
     case DEPTH: {                                                                                              \
         const void* fn = reinterpret_cast<const void*>(&ffn_stream_kernel<DEPTH, EPI>);                        \
         static const hipError_t attr = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax); \
-        if (attr != hipSuccess) return attr;                                                                   \
+        if (attr != hipSuccess) {                                                                              \
+            (void)hipGetLastError(); /* leave no sticky error for later calls */                                \
+            return attr;                                                                                       \
+        }                                                                                                      \
         const int slots = resident_workgroups(fn, lds);                                                        \
         const int upw = slots > 0 ? (units + slots - 1) / slots : 1;                                          \
         ffn_stream_kernel<DEPTH, EPI><<<(units + upw - 1) / upw, kThreads, lds, stream>>>(p, upw);             \
@@ -325,10 +439,16 @@ int stream_down_grid(int E, int H, int I) {
     return E * ((H + kWaves * 32 - 1) / (kWaves * 32)) * pick_shape(I, true).nsplit;
 }
 
-hipError_t launch_ffn_stream(const uint16_t* x, const uint16_t* expert_weights, uint16_t* expert_out,
-                             const FfnWorkspace& ws, int T, int H, int E, int K, int I, hipStream_t stream) {
+hipError_t launch_ffn_stream(const uint16_t* x, const int32_t* expert_ids, const uint16_t* expert_weights,
+                             uint16_t* expert_out, const FfnWorkspace& ws, int T, int H, int E, int K, int I,
+                             hipStream_t stream) {
     StreamArgs p{};
     p.sorted_slot = ws.sorted_slot;
+    p.ids = expert_ids;
+    p.S = T * K;
+    p.offsets_out = ws.offsets;
+    p.sorted_out = ws.sorted_slot;
+    p.expert_out = expert_out;
     p.offsets = ws.offsets;
     p.w = expert_weights;
     p.E = E;

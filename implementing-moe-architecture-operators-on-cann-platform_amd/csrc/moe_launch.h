@@ -58,8 +58,9 @@ bool stream_supported(int H, int I);
 size_t stream_partial_bytes(int T, int H, int K, int I);
 int stream_gateup_grid(int E, int H, int I);
 int stream_down_grid(int E, int H, int I);
-hipError_t launch_ffn_stream(const uint16_t* x, const uint16_t* expert_weights, uint16_t* expert_out,
-                             const FfnWorkspace& ws, int T, int H, int E, int K, int I, hipStream_t stream);
+hipError_t launch_ffn_stream(const uint16_t* x, const int32_t* expert_ids, const uint16_t* expert_weights,
+                             uint16_t* expert_out, const FfnWorkspace& ws, int T, int H, int E, int K, int I,
+                             hipStream_t stream);
 // LDS-tiled schedule (moe_ffn_tiled.hip)
 bool tiled_supported(int H, int I);
 int tiled_block_threads();
@@ -70,8 +71,9 @@ hipError_t launch_ffn_tiled(const uint16_t* x, const uint16_t* expert_weights, u
                             const FfnWorkspace& ws, int T, int H, int E, int K, int I, hipStream_t stream);
 // schedule choice: 0 = weight streaming, 1 = LDS-tiled, -1 = no kernel supports the shape
 int ffn_schedule(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I);
-hipError_t launch_ffn(const uint16_t* x, const uint16_t* expert_weights, uint16_t* expert_out, FfnWorkspace ws,
-                      int T, int H, int E, int K, int I, hipStream_t stream);
+// the whole FFN: permute (tiled schedule; the streaming schedule finds rows itself) and the two GEMMs
+hipError_t launch_ffn(const uint16_t* x, const int32_t* expert_ids, const uint16_t* expert_weights,
+                      uint16_t* expert_out, FfnWorkspace ws, int T, int H, int E, int K, int I, hipStream_t stream);
 
 // ---- combine (moe_combine.hip) ----
 int combine_block_threads();

@@ -246,11 +246,9 @@ moe_status moe_expert_ffn(const uint16_t* x, const int32_t* expert_ids, const ui
         return fail(MOE_ERR_UNSUPPORTED, "MoeExpertFFN: x, expert_weights, expert_out, workspace must be 16-byte aligned");
     const hipStream_t s = as_stream(stream);
     const moe::FfnWorkspace ws = moe::ffn_workspace_carve(workspace, T, H, E, K, I);
-    hipError_t err = moe::launch_permute(expert_ids, static_cast<int>(T * K), static_cast<int>(E), static_cast<int>(H),
-                                         ws, expert_out, s);
-    if (err != hipSuccess) return hip_fail(err, "MoeExpertFFN permute launch");
-    err = moe::launch_ffn(x, expert_weights, expert_out, ws, static_cast<int>(T), static_cast<int>(H),
-                          static_cast<int>(E), static_cast<int>(K), static_cast<int>(I), s);
+    const hipError_t err = moe::launch_ffn(x, expert_ids, expert_weights, expert_out, ws, static_cast<int>(T),
+                                           static_cast<int>(H), static_cast<int>(E), static_cast<int>(K),
+                                           static_cast<int>(I), s);
     if (err != hipSuccess) return hip_fail(err, "MoeExpertFFN GEMM launch");
     return ok();
 }
