@@ -23,7 +23,7 @@ class TraceScope {
 
 // ---- routing (moe_routing.hip) ----
 int routing_expert_blocks(int E);
-int routing_tokens_per_block();
+int routing_tokens_per_block(int E);
 int routing_block_threads(int E);
 int routing_lds_bytes(int E);
 hipError_t launch_routing_topk(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H,
