@@ -246,6 +246,38 @@ def test_ffn_edge_routings(ops):
     within(oracle.compare(eo[mask], eo_o[mask]), max_abs=1e-2, mean_abs=1e-3, cos=0.9999)
 
 
+@pytest.mark.parametrize("T,H,E,K,I,pattern", [
+    (100, 64, 8, 2, 96, "skewed"),      # one expert 150 rows (5 passes of 32), one the rest, six empty
+    (1000, 64, 16, 1, 64, "uniform"),   # S = 1000: each wave's id scan runs several unrolled rounds
+    (37, 128, 64, 3, 160, "invalid"),   # mostly empty experts, ids outside [0, E), I tail (160 = 5 x 32)
+])
+def test_ffn_streaming_schedule_edges(ops, T, H, E, K, I, pattern):
+    """The weight-streaming schedule finds each expert's rows from expert_ids inside its gate/up kernel and
+    writes offsets / sorted_slot for the down kernel: check both and expert_out against the oracle."""
+    assert ffn_schedule(T, H, E, K, I) == 0
+    rng = np.random.default_rng(T + E)
+    x = rng.standard_normal((T, H)).astype(np.float16)
+    ew = np.concatenate([rng.standard_normal((E, 2 * I, H)) / math.sqrt(H),
+                         rng.standard_normal((E, I, H)) / math.sqrt(I)], axis=1).astype(np.float16)
+    if pattern == "skewed":
+        ids = np.full((T, K), 5, np.int32)
+        ids.ravel()[:150] = 2
+    elif pattern == "uniform":
+        ids = rng.integers(0, E, (T, K)).astype(np.int32)
+    else:
+        ids = rng.integers(0, 4, (T, K)).astype(np.int32) * 7  # experts 0, 7, 14, 21
+        ids[3, 1], ids[9, 0], ids[20, 2] = -1, E, 1000
+    w = np.full((T, K), 0.5, np.float16)
+    log(f"[stream edges] {pattern}: T={T} H={H} E={E} K={K} I={I}")
+    eo_d, ws = run_ffn(ops, dev(x), dev(ids), dev(w), dev(ew), I)
+    eo = f32(host(eo_d))
+    check_permute(host(ws), ids, E)
+    valid = (ids >= 0) & (ids < E)
+    assert not eo[~valid].any()
+    eo_o = oracle.expert_ffn(f32(x), np.where(valid, ids, 0), f32(ew), I)
+    within(oracle.compare(eo[valid], eo_o[valid]), max_abs=1e-2, mean_abs=1e-3, cos=0.9999)
+
+
 def test_ffn_rejects_bad_workspace(ops):
     x = dev(np.zeros((4, 64), np.float16))
     ids = dev(np.zeros((4, 2), np.int32))
