@@ -378,16 +378,6 @@ StreamShape pick_shape(int kdim, bool allow_split) {
     return StreamShape{0, 0, 0, 0};  // no layout: the caller reports unsupported
 }
 
-// Workgroups of `kernel` (kThreads threads, `lds` bytes of LDS) resident on the current device at once.
-int resident_workgroups(const void* kernel, size_t lds) {
-    int dev = 0, cus = 0, per_cu = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, lds) != hipSuccess)
-        return 0;
-    return cus * (per_cu > 0 ? per_cu : 1);
-}
-
 template <int EPI>
 hipError_t launch_stream_epi(const StreamArgs& p, int d, int units, hipStream_t stream) {
     const size_t lds = static_cast<size_t>(p.rows_cap) * (p.kc + 8) * sizeof(uint16_t);
@@ -395,12 +385,9 @@ hipError_t launch_stream_epi(const StreamArgs& p, int d, int units, hipStream_t 
 #define MOE_STREAM_CASE(DEPTH)                                                                                 \
     case DEPTH: {                                                                                              \
         const void* fn = reinterpret_cast<const void*>(&ffn_stream_kernel<DEPTH, EPI>);                        \
-        static const hipError_t attr = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax); \
-        if (attr != hipSuccess) {                                                                              \
-            (void)hipGetLastError(); /* leave no sticky error for later calls */                                \
-            return attr;                                                                                       \
-        }                                                                                                      \
-        const int slots = resident_workgroups(fn, lds);                                                        \
+        err = ensure_lds_limit(fn, kLdsMax);                                                                   \
+        if (err != hipSuccess) return err;                                                                     \
+        const int slots = resident_workgroups(fn, kThreads, lds);                                              \
         const int upw = slots > 0 ? (units + slots - 1) / slots : 1;                                          \
         ffn_stream_kernel<DEPTH, EPI><<<(units + upw - 1) / upw, kThreads, lds, stream>>>(p, upw);             \
         break;                                                                                                 \

@@ -208,12 +208,8 @@ __global__ __launch_bounds__(kThreads) void ffn_tiled_kernel(TiledArgs p) {
 
 template <int EPI>
 hipError_t launch_tiled(const TiledArgs& p, int grid, hipStream_t stream) {
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&ffn_tiled_kernel<EPI>),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
-    if (attr != hipSuccess) {
-        (void)hipGetLastError();  // leave no sticky error for later calls
-        return attr;
-    }
+    const hipError_t attr = ensure_lds_limit(reinterpret_cast<const void*>(&ffn_tiled_kernel<EPI>), kLdsBytes);
+    if (attr != hipSuccess) return attr;
     ffn_tiled_kernel<EPI><<<grid, kThreads, kLdsBytes, stream>>>(p);
     return hipGetLastError();
 }

@@ -21,6 +21,14 @@ class TraceScope {
     hipEvent_t start_ = nullptr;
 };
 
+// ---- per-device launch preparation (moe_runtime.cpp) ----
+// Raises kernel `fn`'s dynamic-LDS limit to `lds_max` bytes on the current device (once per device and kernel;
+// needed above 64 KB). Returns the HIP error of that call, hipSuccess when it was already done.
+hipError_t ensure_lds_limit(const void* fn, int lds_max);
+// Workgroups of `fn` (`threads` threads, `lds` bytes of dynamic LDS) the current device holds at once, cached per
+// device, kernel and LDS size; 0 when the device cannot be queried.
+int resident_workgroups(const void* fn, int threads, size_t lds);
+
 // ---- routing (moe_routing.hip) ----
 int routing_expert_blocks(int E);
 int routing_tokens_per_block(int E);

@@ -330,13 +330,9 @@ hipError_t launch_wide(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, 
                        int K, hipStream_t stream) {
     const int grid = (T + kWideTokens - 1) / kWideTokens;
     const size_t lds = wide_lds_bytes(EB);
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&routing_wide_kernel<EB>),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                       static_cast<int>(lds));
-    if (attr != hipSuccess) {
-        (void)hipGetLastError();  // leave no sticky error for later calls
-        return attr;
-    }
+    const hipError_t attr = ensure_lds_limit(reinterpret_cast<const void*>(&routing_wide_kernel<EB>),
+                                             static_cast<int>(lds));
+    if (attr != hipSuccess) return attr;
     TraceScope trace("moe_routing_topk", stream);
     routing_wide_kernel<EB><<<grid, kWideWaves * kWave, lds, stream>>>(x, w_gate, ids, w, T, H, E, K);
     return hipGetLastError();
