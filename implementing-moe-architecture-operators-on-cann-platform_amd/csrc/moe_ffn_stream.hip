@@ -10,7 +10,8 @@
 //   * activation loads issued through the same vector-memory queue cost 10-40%: loads retire in order and the
 //     L2-served traffic competes with the HBM stream -> activations are staged in LDS once per workgroup;
 //   * all waves walking the rows in the same k order hit the same address-mod-4KB at the same time (rows are
-//     4 KB / 16 KB apart): starting each wave at a different k (rotation) is worth ~10%;
+//     4 KB / 16 KB apart): starting each wave at a different k (rotation) is worth ~10% in a pure-load kernel
+//     (5.4 -> 6.1 TB/s) though only ~1% in this one, whose remaining gap to the pure-load rate is structural;
 //   * register spills in the loop are fatal: scratch reloads also wait on the vector-memory counter and drain
 //     the weight ring -> 8 waves per workgroup, no spills (checked with -Rpass-analysis=kernel-resource-usage).
 //

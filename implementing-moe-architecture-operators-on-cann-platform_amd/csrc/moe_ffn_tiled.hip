@@ -3,8 +3,12 @@
 // Reference: op_kernel/moe_expert_ffn.cpp (ComputeSwiGLU :265-333, ComputeDownProj :339-394, scatter :250-257);
 // oracle: tests/moe_cpu_sim.cpp:245-296 (W_gate, W_up [I, H]; W_down [H, I]).
 //
-// With ~1000 rows per expert (T = 8192, K = 2, E = 16) the GEMMs are MFMA-bound. Both are "NT": activation rows
-// and weight rows are contiguous along the reduction dim k.
+// With ~1000 rows per expert (T = 8192, K = 2, E = 16) the GEMMs have an arithmetic intensity of ~1500 flop/B
+// against HBM, far above the MFMA ridge. Both are "NT": activation rows and weight rows are contiguous along the
+// reduction dim k. Measured on MI355X, the limit is operand movement into the CUs rather than the MFMAs: the
+// same kernel with its MFMAs replaced by a trivial use of the fragments takes ~80% of the full kernel's time,
+// and its global loads alone ~80% too (a 256 x 256 tile brings 1/128 B per flop into the CU, mostly from the
+// Infinity Cache and HBM).
 //   macro tile   256 activation rows x 256 weight rows x 64 k per stage; 8 waves (2 x 4), each a 128 x 64
 //                sub-tile (8 x 4 v_mfma_f32_16x16x32_f16 tiles, 128 fp32 accumulators per lane: with 256 per
 //                lane the accumulators plus the loop's other live values exceed one wave's register file and
