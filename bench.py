@@ -21,6 +21,7 @@ The JSON line also carries:
                 them for this workload, else null;
   cpu_baseline  the reference's own NaiveMoE (tests/moe_cpu_sim.cpp, built from its source into oracle/_ref),
                 single-threaded on this host, on the first tokens of the same inputs, scaled to a whole layer;
+                cpu_baseline_tiled is its TiledMoE on the same sample;
   accuracy      this run's y on those tokens against that NaiveMoE output (the reference's thresholds).
 """
 from __future__ import annotations
@@ -232,6 +233,7 @@ def main() -> int:
     roofline = roofline_for(dominant, db, dflops, kernels[dominant][1] / kernels[dominant][0], traffic)
 
     cpu_baseline = None
+    cpu_baseline_tiled = None
     accuracy = None
     if not args.no_cpu_baseline:
         import oracle
@@ -244,7 +246,14 @@ def main() -> int:
             wg_h = wg.float().cpu().numpy()
             ew_h = ew.cpu().numpy().astype(np.float32)
             y_ref, ref_ms = oracle.ref_moe_timed(x_s, wg_h, ew_h, K, I)
+            y_tiled, tiled_ms = oracle.ref_moe_timed(x_s, wg_h, ew_h, K, I, tiled=True)
             del ew_h
+            cpu_baseline_tiled = {"value": round(tiled_ms * 1e3 * T / n_s, 1), "unit": "us", "cores": 1,
+                                  "kind": "reference",
+                                  "sample": f"TiledMoE (tests/moe_cpu_sim.cpp:315-569) on the same {n_s} tokens; "
+                                            f"{tiled_ms:.0f} ms scaled by {T}/{n_s}"}
+            m_t = oracle.compare(y_tiled, y_ref)
+            progress(f"cpu baseline (tiled) {tiled_ms:.0f} ms; tiled vs naive max_abs {m_t['max_abs']:.2e}")
             cpu_baseline = {"value": round(ref_ms * 1e3 * T / n_s, 1), "unit": "us", "cores": 1, "kind": "reference",
                             "sample": f"NaiveMoE (tests/moe_cpu_sim.cpp:183-306, g++ -O2 -std=c++17) on the first "
                                       f"{n_s} of {T} tokens, all {E} experts' weights; {ref_ms:.0f} ms scaled by "
@@ -284,6 +293,7 @@ def main() -> int:
         "kernels": per_kernel,
         "roofline": roofline,
         "cpu_baseline": cpu_baseline,
+        "cpu_baseline_tiled": cpu_baseline_tiled,
         "accuracy": accuracy,
     }
     print(json.dumps(result), flush=True)
