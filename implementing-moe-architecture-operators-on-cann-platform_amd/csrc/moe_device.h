@@ -43,4 +43,13 @@ __device__ __forceinline__ f32x4 mfma16x16x32(f16x8 a, f16x8 b, f32x4 c) {
 
 __device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x) & (kWave - 1); }
 
+// SwiGLU of one fp32 (gate, up) pair: silu(g) * u = g / (1 + exp(-g)) * u. Contraction into FMAs is off, so each
+// operation rounds on its own and the result does not depend on how the compiler schedules the code around it
+// (with contraction on, unrolled copies of the same epilogue were seen to round differently).
+__device__ __forceinline__ float swiglu_f32(float g, float u) {
+#pragma clang fp contract(off)
+    const float silu = g / (1.0f + expf(-g));
+    return silu * u;
+}
+
 }  // namespace moe

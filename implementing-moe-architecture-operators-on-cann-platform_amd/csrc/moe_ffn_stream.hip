@@ -5,15 +5,24 @@
 //
 // With few rows per expert (decode: T = 128, K = 2, E = 16 -> ~16 rows) each weight byte serves only those
 // rows, so the GEMMs are bound by streaming E*3*I*H*2 bytes from HBM once. What the MI355X measurements behind
-// this design showed (pure load kernels at the real [E, 3I, H] layout):
-//   * a wave streaming weight rows with D k-steps of loads in flight sustains ~6 TB/s, even at 2 waves/SIMD;
+// this design showed (pure load kernels reading the 1.07 GB of decode gate/up weights at the real [E, 3I, H]
+// layout, 8 waves per CU, 16 KB in flight per wave):
+//   * the shape of one load instruction decides the rate. Loading straight into the MFMA operand order puts
+//     16 weight rows x 64 B (half a 128-B line each) in every instruction and tops out at ~5.8 TB/s with any
+//     cache policy (5.3 TB/s non-temporal). Whole lines do better only when also non-temporal: 8 rows x 128 B
+//     6.5 TB/s, 1 row x 1 KB 7.0 TB/s; without the non-temporal hint every shape stays at ~5.9 TB/s;
+//   * so each 64-k column block of a tile is loaded as two non-temporal 8-row x 128-B instructions and each
+//     wave re-lays it into the MFMA order through 2 KB of its own LDS (one write, one read per 16 B; 6.85 TB/s
+//     in the pure-load kernel with the re-layout included). Wider shapes need more LDS per wave than is left
+//     beside the 128 KB activation stage;
 //   * activation loads issued through the same vector-memory queue cost 10-40%: loads retire in order and the
 //     L2-served traffic competes with the HBM stream -> activations are staged in LDS once per workgroup;
 //   * all waves walking the rows in the same k order hit the same address-mod-4KB at the same time (rows are
-//     4 KB / 16 KB apart): starting each wave at a different k (rotation) is worth ~10% in a pure-load kernel
-//     (5.4 -> 6.1 TB/s) though only ~1% in this one, whose remaining gap to the pure-load rate is structural;
+//     4 KB / 16 KB apart): each wave starts at a different column block (rotation);
 //   * register spills in the loop are fatal: scratch reloads also wait on the vector-memory counter and drain
-//     the weight ring -> 8 waves per workgroup, no spills (checked with -Rpass-analysis=kernel-resource-usage).
+//     the weight ring -> 8 waves per workgroup, no spills (checked with -Rpass-analysis=kernel-resource-usage);
+//   * what did not pay: issuing the next unit's first loads before this unit's epilogue (slower by 3%), and
+//     pinning the load / MFMA interleave of the ring with scheduling barriers (slower by 1.5%).
 //
 // Work unit = one expert e, one K-range [k0, k0 + kc) and one column group (8 waves x 16 or 32 weight rows).
 // The grid is persistent: as many 8-wave workgroups as the GPU holds at once, each taking a contiguous run of
@@ -26,8 +35,10 @@
 //      the K-range of the pass's activation rows (up to 32; x rows gathered by slot / K for gate/up, SwiGLU rows
 //      for down) into LDS, then one barrier;
 //   3. each wave streams two 16-row weight tiles (gate/up: W_gate and W_up rows n0..n0+15; down: W_down rows
-//      n0..n0+31) through a register ring of D k-steps, starting at its own rotated step, with activation
-//      fragments read from LDS (ds_read_b128) and v_mfma_f32_16x16x32_f16 (fp32 accumulation);
+//      n0..n0+31) through a register ring of D/2 column blocks (D k-steps of 32), starting at its own rotated
+//      block; per block: the four whole-line loads go through the wave's LDS re-layout buffer, activation
+//      fragments come from the LDS stage (ds_read_b128), v_mfma_f32_16x16x32_f16 (fp32 accumulation).
+//      With kc = 32 (D = 1) the loads go straight into the MFMA order instead (register ring of D k-steps);
 //   4. epilogue in registers: gate/up -> hidden = silu(gate) * up (fp32) -> fp16 workspace row;
 //      down with one K-range -> expert_out[slot] fp16 (the scatter back to [T, K, H] order);
 //      down with several K-ranges -> fp32 partial sums, added in a fixed order by down_reduce_kernel (no atomics,
@@ -39,7 +50,7 @@
 // An expert with more than 32 rows takes several passes, each re-streaming the weights: this schedule is
 // chosen only when the average number of rows per expert is small.
 // LDS: row r of the staged K-range at r * (kc + 8) halfs (16 B of padding per row puts the 16 rows read by one
-// ds_read_b128 in different banks).
+// ds_read_b128 in different banks), then the eight 2 KB re-layout buffers.
 
 #include "moe_device.h"
 #include "moe_launch.h"
@@ -52,6 +63,8 @@ constexpr int kWaves = 8;                 // streaming waves per workgroup
 constexpr int kThreads = kWaves * kWave;  // 512
 constexpr int kMaxRows = 32;              // activation rows per pass (two 16-row MFMA tiles)
 constexpr int kLdsMax = 160 * 1024 - 1024;  // gfx950 LDS per workgroup, less 1 KB for the static arrays
+
+constexpr int kTbBytes = kWaves * 2048;     // per-wave 2 KB re-layout buffers of the full-line ring
 
 enum Epilogue { kSwiGLU = 0, kScatter = 1, kPartial = 2 };
 
@@ -85,8 +98,6 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-__device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)); }
-
 // D k-steps on ring slots 0..D-1: activation fragments from LDS at physical step `ph`, then (REFILL) reload
 // each slot with physical step `pn` + i.
 template <int MT, int D, bool REFILL>
@@ -111,6 +122,32 @@ __device__ __forceinline__ void ring_batch(const uint16_t* lds, int stride, int 
     }
 }
 
+// D[m][n]: m = 4*kg + j (activation row of tile mt), n = row (weight row of the tile)
+template <int MT, int EPI>
+__device__ __forceinline__ void epilogue(const StreamArgs& p, const f32x4 (&acc0)[MT], const f32x4 (&acc1)[MT],
+                                         int off, int ne, int mc, int n0, int split, int lane) {
+    const int row = lane & 15, kg = lane >> 4;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int m = mc + mt * 16 + kg * 4 + j;
+            if (m >= ne) continue;
+            if (EPI == kSwiGLU) {
+                const float hv = swiglu_f32(acc0[mt][j], acc1[mt][j]);
+                p.out[static_cast<size_t>(off + m) * p.ndim + n0 + row] = f32_to_f16_bits(hv);
+            } else if (EPI == kScatter) {
+                const size_t o = static_cast<size_t>(p.sorted_slot[off + m]) * p.ndim + n0 + row;
+                p.out[o] = f32_to_f16_bits(acc0[mt][j]);
+                p.out[o + 16] = f32_to_f16_bits(acc1[mt][j]);
+            } else {
+                float* dst = p.partial + (static_cast<size_t>(split) * p.total_rows + off + m) * p.ndim + n0 + row;
+                dst[0] = acc0[mt][j];
+                dst[16] = acc1[mt][j];
+            }
+        }
+}
+
 // Whole K-range of one pass for one wave; the ring was primed by the caller at step `rot`.
 template <int MT, int D, int EPI>
 __device__ __forceinline__ void ring_pass(const StreamArgs& p, const uint16_t* lds, const uint16_t* w0,
@@ -133,26 +170,77 @@ __device__ __forceinline__ void ring_pass(const StreamArgs& p, const uint16_t* l
         else
             ring_batch<MT, D, false>(lds, stride, ph, pn, row, kg, w0, w1, r0, r1, acc0, acc1);
     }
-    // D[m][n]: m = 4*kg + j (activation row of tile mt), n = row (weight row of the tile)
+    epilogue<MT, EPI>(p, acc0, acc1, off, ne, mc, n0, split, lane);
+}
+
+// Full-line ring: a column block is 64 k of both tiles (two MFMA steps), loaded as four non-temporal
+// instructions that each cover 8 whole weight rows x 128 B: tile 0 rows 0-7, tile 0 rows 8-15, tile 1 rows 0-7,
+// tile 1 rows 8-15 (lane -> row lane / 8, 16 B chunk lane % 8). The wave then re-lays each tile through its own
+// 2 KB of LDS into the MFMA B order (row lane % 16, chunk 4 * step + lane / 16).
+// Buffer: row r, chunk c at r * 128 + ((c ^ ((r >> 1) & 7)) * 16) bytes -> conflict-free writes and reads.
+__device__ __forceinline__ int tb_off(int r, int c) { return r * 64 + ((c ^ ((r >> 1) & 7)) * 8); }  // halfs
+
+template <int CB>
+__device__ __forceinline__ void line_prime(const uint16_t* const (&wr)[4], int rotb, f16x8 (&rg)[CB][4]) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int i = 0; i < CB; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int m = mc + mt * 16 + kg * 4 + j;
-            if (m >= ne) continue;
-            if (EPI == kSwiGLU) {
-                const float hv = silu_f32(acc0[mt][j]) * acc1[mt][j];
-                p.out[static_cast<size_t>(off + m) * p.ndim + n0 + row] = f32_to_f16_bits(hv);
-            } else if (EPI == kScatter) {
-                const size_t o = static_cast<size_t>(p.sorted_slot[off + m]) * p.ndim + n0 + row;
-                p.out[o] = f32_to_f16_bits(acc0[mt][j]);
-                p.out[o + 16] = f32_to_f16_bits(acc1[mt][j]);
-            } else {
-                float* dst = p.partial + (static_cast<size_t>(split) * p.total_rows + off + m) * p.ndim + n0 + row;
-                dst[0] = acc0[mt][j];
-                dst[16] = acc1[mt][j];
+        for (int j = 0; j < 4; ++j) rg[i][j] = load_f16x8_stream(wr[j] + (rotb + i) * 64);
+}
+
+template <int MT, int CB, int EPI>
+__device__ __forceinline__ void line_pass(const StreamArgs& p, const uint16_t* lds, uint16_t* tb,
+                                          const uint16_t* const (&wr)[4], f16x8 (&rg)[CB][4], int rotb, int off,
+                                          int ne, int mc, int n0, int split, int lane) {
+    const int row = lane & 15, kg = lane >> 4;
+    const int nblk = p.kc / 64;
+    const int stride = p.kc + 8;
+    const int wrow = lane >> 3, wc = lane & 7;
+    f32x4 acc0[MT], acc1[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        acc0[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        acc1[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    for (int b0 = 0; b0 < nblk; b0 += CB) {
+#pragma unroll
+        for (int i = 0; i < CB; ++i) {
+            const int ph = b0 + i + rotb < nblk ? b0 + i + rotb : b0 + i + rotb - nblk;
+            f16x8 bf[2][2];
+#pragma unroll
+            for (int m = 0; m < 2; ++m) {
+                *reinterpret_cast<f16x8*>(tb + tb_off(wrow, wc)) = rg[i][2 * m];
+                *reinterpret_cast<f16x8*>(tb + tb_off(8 + wrow, wc)) = rg[i][2 * m + 1];
+                // the reads below take what other lanes of this wave just wrote: keep the compiler from moving
+                // them above the writes (LDS operations of one wave execute in order, so no wait is needed)
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                bf[m][0] = *reinterpret_cast<const f16x8*>(tb + tb_off(row, kg));
+                bf[m][1] = *reinterpret_cast<const f16x8*>(tb + tb_off(row, 4 + kg));
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // reads done before the next writes
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
             }
+            if (b0 + CB < nblk) {
+                const int pn = ph + CB < nblk ? ph + CB : ph + CB - nblk;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) rg[i][j] = load_f16x8_stream(wr[j] + pn * 64);
+            }
+#pragma unroll
+            for (int st = 0; st < 2; ++st) {
+                f16x8 a[MT];
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+                    a[mt] = *reinterpret_cast<const f16x8*>(lds + (mt * 16 + row) * stride + (2 * ph + st) * 32 + kg * 8);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    acc0[mt] = mfma16x16x32(a[mt], bf[0][st], acc0[mt]);
+                    acc1[mt] = mfma16x16x32(a[mt], bf[1][st], acc1[mt]);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
+    }
+    epilogue<MT, EPI>(p, acc0, acc1, off, ne, mc, n0, split, lane);
 }
 
 // Expert e's rows by scanning ids: wave w takes the contiguous chunk w of the T*K slots.
@@ -282,14 +370,26 @@ __global__ __launch_bounds__(kThreads) void ffn_stream_kernel(StreamArgs p, int 
         const uint16_t* w1 = w0 + p.w1_off;
         const int rot = ((u * kWaves + wave) * 7 * D) % nsteps;  // a multiple of D: batches never wrap
 
+        constexpr int CB = D / 2;  // column blocks in flight (full-line ring, D >= 2)
+        constexpr int CBn = CB > 0 ? CB : 1;
+        const uint16_t* wbase = p.w + ebase + p.w_off + static_cast<size_t>(active ? n0 : 0) * p.kdim + k0 +
+                                static_cast<size_t>(lane >> 3) * p.kdim + (lane & 7) * 8;
+        const uint16_t* const wr[4] = {wbase, wbase + static_cast<size_t>(8) * p.kdim, wbase + p.w1_off,
+                                       wbase + p.w1_off + static_cast<size_t>(8) * p.kdim};
+
         for (int mc = 0; mc < ne; mc += p.rows_cap) {
             const int rows = min(p.rows_cap, ne - mc);
             f16x8 r0[D], r1[D];
+            f16x8 rg[CBn][4];
             if (active) {
+                if (CB > 0) {
+                    line_prime<CBn>(wr, rot / 2, rg);
+                } else {
 #pragma unroll
-                for (int i = 0; i < D; ++i) {
-                    r0[i] = load_f16x8(w0 + (rot + i) * 32);
-                    r1[i] = load_f16x8(w1 + (rot + i) * 32);
+                    for (int i = 0; i < D; ++i) {
+                        r0[i] = load_f16x8(w0 + (rot + i) * 32);
+                        r1[i] = load_f16x8(w1 + (rot + i) * 32);
+                    }
                 }
             }
             if (e != staged_e || split != staged_split || mc != staged_mc) {
@@ -324,10 +424,17 @@ __global__ __launch_bounds__(kThreads) void ffn_stream_kernel(StreamArgs p, int 
                 lds_barrier();
             }
             if (active) {
-                if (rows > 16)
+                if (CB > 0) {
+                    uint16_t* tb = lds + p.rows_cap * stride + wave * 1024;
+                    if (rows > 16)
+                        line_pass<2, CBn, EPI>(p, lds, tb, wr, rg, rot / 2, off, ne, mc, n0, split, lane);
+                    else
+                        line_pass<1, CBn, EPI>(p, lds, tb, wr, rg, rot / 2, off, ne, mc, n0, split, lane);
+                } else if (rows > 16) {
                     ring_pass<2, D, EPI>(p, lds, w0, w1, r0, r1, rot, off, ne, mc, n0, split, lane);
-                else
+                } else {
                     ring_pass<1, D, EPI>(p, lds, w0, w1, r0, r1, rot, off, ne, mc, n0, split, lane);
+                }
             }
         }
 
@@ -368,7 +475,7 @@ struct StreamShape {
 
 StreamShape pick_shape(int kdim, bool allow_split) {
     for (int rows_cap : {kMaxRows, 16}) {
-        const int kc_max = kLdsMax / (rows_cap * 2) - 8;
+        const int kc_max = (kLdsMax - kTbBytes) / (rows_cap * 2) - 8;
         for (int d = 8; d >= 1; d /= 2) {
             int best = 0;
             for (int kc = 32 * d; kc <= kc_max && kc <= kdim; kc += 32 * d)
@@ -381,7 +488,7 @@ StreamShape pick_shape(int kdim, bool allow_split) {
 
 template <int EPI>
 hipError_t launch_stream_epi(const StreamArgs& p, int d, int units, hipStream_t stream) {
-    const size_t lds = static_cast<size_t>(p.rows_cap) * (p.kc + 8) * sizeof(uint16_t);
+    const size_t lds = static_cast<size_t>(p.rows_cap) * (p.kc + 8) * sizeof(uint16_t) + (d >= 2 ? kTbBytes : 0);
     hipError_t err = hipSuccess;
 #define MOE_STREAM_CASE(DEPTH)                                                                                 \
     case DEPTH: {                                                                                              \

@@ -64,8 +64,6 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-__device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)); }
-
 // Linear tile -> (expert, m-tile, n-tile); false when t is past the last tile.
 __device__ __forceinline__ bool find_tile(const TiledArgs& p, int t, int* e_out, int* mt_out, int* nt_out,
                                           int* off_out, int* ne_out) {
@@ -197,7 +195,7 @@ __global__ __launch_bounds__(kThreads) void ffn_tiled_kernel(TiledArgs p) {
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
                     const int col = nt * 128 + wn * 32 + j * 16 + row16;
-                    if (col < p.I) dst[col] = f32_to_f16_bits(silu_f32(acc[i][j][r]) * acc[i][j + 2][r]);
+                    if (col < p.I) dst[col] = f32_to_f16_bits(swiglu_f32(acc[i][j][r], acc[i][j + 2][r]));
                 }
             } else {
                 uint16_t* dst = p.out + static_cast<size_t>(p.sorted_slot[off + m]) * p.H;
