@@ -250,6 +250,10 @@ def test_ffn_edge_routings(ops):
     (100, 64, 8, 2, 96, "skewed"),      # one expert 150 rows (5 passes of 32), one the rest, six empty
     (1000, 64, 16, 1, 64, "uniform"),   # S = 1000: each wave's id scan runs several unrolled rounds
     (37, 128, 64, 3, 160, "invalid"),   # mostly empty experts, ids outside [0, E), I tail (160 = 5 x 32)
+    # ring depths of the whole-line weight stream (D k-steps = D/2 column blocks of 64 k):
+    (64, 256, 8, 2, 512, "uniform"),    # gate/up D = 8, down D = 8 in one K-range (scatter epilogue)
+    (48, 128, 8, 2, 384, "uniform"),    # gate/up D = 4, down D = 4 in one K-range
+    (40, 512, 4, 2, 2560, "uniform"),   # down D = 8 over 2 K-ranges of 1280 (partials + reduce)
 ])
 def test_ffn_streaming_schedule_edges(ops, T, H, E, K, I, pattern):
     """The weight-streaming schedule finds each expert's rows from expert_ids inside its gate/up kernel and
