@@ -5,10 +5,10 @@
 //
 // With ~1000 rows per expert (T = 8192, K = 2, E = 16) the GEMMs have an arithmetic intensity of ~1500 flop/B
 // against HBM, far above the MFMA ridge. Both are "NT": activation rows and weight rows are contiguous along the
-// reduction dim k. Measured on MI355X, the limit is operand movement into the CUs rather than the MFMAs: the
-// same kernel with its MFMAs replaced by a trivial use of the fragments takes ~80% of the full kernel's time,
-// and its global loads alone ~80% too (a 256 x 256 tile brings 1/128 B per flop into the CU, mostly from the
-// Infinity Cache and HBM).
+// reduction dim k. Measured on MI355X with stripped copies of this kernel: its global loads alone take ~44% of
+// its time (12 TB/s from L2), its MFMAs alone ~32%, but LDS stores + fragment reads + MFMAs without any global
+// load already ~82%. Per 64-k stage a CU moves 256 KB through LDS against 2048 MFMA cycles per SIMD, and the two
+// overlap poorly: the LDS side, not the memory system, is what a faster schedule has to shrink.
 //   macro tile   256 activation rows x 256 weight rows x 64 k per stage; 8 waves (2 x 4), each a 128 x 64
 //                sub-tile (8 x 4 v_mfma_f32_16x16x32_f16 tiles, 128 fp32 accumulators per lane: with 256 per
 //                lane the accumulators plus the loop's other live values exceed one wave's register file and
