@@ -7,12 +7,15 @@ T=128, H=2048, E=16, K=2, I=8192 (fp16 I/O, fp32 accumulation) by default.
 A step is one pass of the layer over one batch of synthetic input resident in HBM: routing, the expert FFN
 (permute + fused gate/up/SwiGLU grouped GEMM + down grouped GEMM with the expert_out scatter) and combine, all
 through the C ABI of libmoe_mi355x.so on one stream, with caller-owned buffers allocated once.
-W warm-up steps, then three timed passes of K steps each, every pass between torch.cuda.synchronize() calls:
+W warm-up steps, then four timed passes of K steps each, every pass between torch.cuda.synchronize() calls:
   1. eager: the three C-ABI calls per step, nothing else recorded -> `value` and `ms_per_step`;
   2. graph replay: the same three calls captured once in a HIP graph, replayed K times (y checked bit-exact
      against the eager y first) -> `layer_us_graph_replay`;
   3. traced: eager again, with HIP events that the library records around each of its launches on the launch
      stream -> per-kernel average durations, from which `roofline` is computed.
+  4. fused: routing, then moe_expert_ffn_combine (the FFN and the combine in one call, an optional fast path;
+     expert_out and y checked bit-exact against the three-operator layer first) -> `layer_us_fused_ffn_combine`.
+     `value` stays the three-operator layer, the drop-in pipeline.
 
 The JSON line also carries:
   roofline      the dominant kernel's algorithmic bytes (or flops) per launch / its average event-timed
@@ -209,6 +212,23 @@ def main() -> int:
     with ops.kernel_trace() as kernels:
         traced_ms, _ = timed(step)
     progress(f"traced: {traced_ms * 1e3:.1f} us/step with an event pair around every launch")
+    # 4) the optional fast path: routing, then the FFN and the combine in one call (moe_expert_ffn_combine);
+    #    y and expert_out must equal the three-operator layer's bit for bit
+    def step_fused(s: int = sp) -> None:
+        st = lib.moe_routing_topk(p["x"], p["wg"], p["ids"], p["w"], T, H, E, K, s)
+        st |= lib.moe_expert_ffn_combine(p["x"], p["ids"], p["w"], p["ew"], p["eo"], p["y"], p["ws"], ws_bytes,
+                                         T, H, E, K, I, s)
+        if st:
+            raise RuntimeError(lib.moe_last_error().decode())
+
+    eo_eager = eo.clone()
+    y.zero_()
+    step_fused()
+    torch.cuda.synchronize()
+    if not (torch.equal(y, y_eager) and torch.equal(eo, eo_eager)):
+        raise RuntimeError("the fused FFN + combine differs from the three-operator layer")
+    fused_ms, fused_gpu_ms = timed(step_fused)
+    progress(f"fused FFN + combine: {fused_ms * 1e3:.1f} us/step (host clock), {fused_gpu_ms * 1e3:.1f} us/step (events)")
 
     ids_h = ids.cpu().numpy()
     active = int((np.bincount(ids_h.ravel(), minlength=E) > 0).sum())
@@ -285,6 +305,7 @@ def main() -> int:
         "layer_us_gpu_events": round(gpu_ms_per_step * 1e3, 2),
         "layer_us_graph_replay": round(graph_ms * 1e3, 2) if graph_ms else None,
         "layer_us_traced": round(traced_ms * 1e3, 2),
+        "layer_us_fused_ffn_combine": round(fused_ms * 1e3, 2),
         "ffn_us": round(ffn_ms * 1e3, 2),
         "ffn_tflops": round(ffn_flops / (ffn_ms * 1e-3) / 1e12, 2),
         "ffn_hbm_gbps": round(ffn_bytes / (ffn_ms * 1e-3) / 1e9, 1),

@@ -33,21 +33,23 @@ int ffn_schedule(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
     return -1;
 }
 
-// Layout (each region 256-byte aligned): offsets [E+1] i32 | sorted_slot [T*K] i32 | hidden [T*K, I] fp16 |
-// partial [nsplit, T*K, H] fp32 (weight-streaming schedule, when the down projection is split over K).
+// Layout (each region 256-byte aligned): offsets [E+1] i32 | sorted_slot [T*K] i32 | hidden [T*K, I] fp16, then
+// for the weight-streaming schedule: partial [nsplit, T*K, H] fp32 (when the down projection is split over K) |
+// slot_row [T*K] i32.
 size_t ffn_workspace_bytes(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
     const size_t S = static_cast<size_t>(T) * static_cast<size_t>(K);
     size_t bytes = align_up(sizeof(int32_t) * static_cast<size_t>(E + 1), 256);
     bytes += align_up(sizeof(int32_t) * S, 256);
     bytes += align_up(sizeof(uint16_t) * S * static_cast<size_t>(I), 256);
-    if (ffn_schedule(T, H, E, K, I) == 0)
+    if (ffn_schedule(T, H, E, K, I) == 0) {
         bytes += align_up(stream_partial_bytes(static_cast<int>(T), static_cast<int>(H), static_cast<int>(K),
                                                static_cast<int>(I)), 256);
+        bytes += align_up(sizeof(int32_t) * S, 256);
+    }
     return bytes;
 }
 
 FfnWorkspace ffn_workspace_carve(void* base, int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
-    (void)H;
     const size_t S = static_cast<size_t>(T) * static_cast<size_t>(K);
     char* p = static_cast<char*>(base);
     FfnWorkspace ws;
@@ -58,6 +60,12 @@ FfnWorkspace ffn_workspace_carve(void* base, int64_t T, int64_t H, int64_t E, in
     ws.hidden = reinterpret_cast<uint16_t*>(p);
     p += align_up(sizeof(uint16_t) * S * static_cast<size_t>(I), 256);
     ws.partial = reinterpret_cast<float*>(p);
+    ws.slot_row = nullptr;
+    if (ffn_schedule(T, H, E, K, I) == 0) {
+        p += align_up(stream_partial_bytes(static_cast<int>(T), static_cast<int>(H), static_cast<int>(K),
+                                           static_cast<int>(I)), 256);
+        ws.slot_row = reinterpret_cast<int32_t*>(p);
+    }
     return ws;
 }
 
@@ -89,6 +97,16 @@ hipError_t launch_ffn(const uint16_t* x, const int32_t* expert_ids, const uint16
         case 0: return launch_ffn_stream(x, expert_ids, expert_weights, expert_out, ws, T, H, E, K, I, stream);
         default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_ffn_combine(const uint16_t* x, const int32_t* expert_ids, const uint16_t* weights,
+                              const uint16_t* expert_weights, uint16_t* expert_out, uint16_t* y, FfnWorkspace ws,
+                              int T, int H, int E, int K, int I, hipStream_t stream) {
+    if (ffn_schedule(T, H, E, K, I) == 0)
+        return launch_ffn_stream(x, expert_ids, expert_weights, expert_out, ws, T, H, E, K, I, stream, weights, y);
+    const hipError_t err = launch_ffn(x, expert_ids, expert_weights, expert_out, ws, T, H, E, K, I, stream);
+    if (err != hipSuccess) return err;
+    return launch_combine(expert_out, weights, y, T, H, K, stream);
 }
 
 }  // namespace moe

@@ -89,6 +89,7 @@ struct StreamArgs {
     int S;                        // T*K
     int32_t* offsets_out;         // gate/up writes offsets [E+1] and sorted_slot [T*K] for the down kernel
     int32_t* sorted_out;
+    int32_t* slot_row_out;        // and the inverse: slot_row[slot] = sorted row, for the slots of valid ids
     uint16_t* expert_out;         // gate/up zeroes the rows of ids outside [0, E)
 };
 
@@ -246,7 +247,7 @@ __device__ __forceinline__ void line_pass(const StreamArgs& p, const uint16_t* l
 // Expert e's rows by scanning ids: wave w takes the contiguous chunk w of the T*K slots.
 // count: per-wave numbers of ids == e and of valid ids < e into s_eq / s_lt (the caller then barriers);
 // rank:  the slots of e in ascending order get ranks 0..ne-1; those in [mc, mc + cap) go to s_rows, and with
-//        `sorted` non-null every slot is written to sorted[off + rank].
+//        `sorted` non-null every slot is written to sorted[off + rank] and off + rank to slot_row[slot].
 __device__ __forceinline__ void expert_count(const StreamArgs& p, int e, int* s_eq, int* s_lt) {
     const int wave = static_cast<int>(threadIdx.x) / kWave, lane = lane_id();
     const int chunk = ((p.S + kWaves - 1) / kWaves + kWave - 1) / kWave * kWave;
@@ -292,7 +293,10 @@ __device__ __forceinline__ void expert_rank(const StreamArgs& p, int e, int befo
                 const int rank = pos + __popcll(m & below);
                 const int sl = base + u * kWave + lane;
                 if (rank >= mc && rank < mc + cap) s_rows[rank - mc] = sl;
-                if (sorted) sorted[off + rank] = sl;
+                if (sorted) {
+                    sorted[off + rank] = sl;
+                    p.slot_row_out[sl] = off + rank;
+                }
             }
             pos += __popcll(m);
         }
@@ -467,6 +471,58 @@ __global__ __launch_bounds__(256) void down_reduce_kernel(const float* __restric
     *reinterpret_cast<f16x8*>(expert_out + static_cast<size_t>(sorted_slot[r]) * H + c) = o;
 }
 
+// The split reduce fused with MoeCombine, one thread per (token, 8 columns): for k ascending, expert_out row
+// (t, k) = fp16 of the partials added in split order, exactly as down_reduce_kernel writes it, and
+// y[t] = sum_k weights[t, k] * expert_out[t, k] with the combine kernel's fp32 arithmetic (accumulator from 0,
+// k ascending, no contraction), so y is bit-identical to MoeCombine on that expert_out. Rows of ids outside
+// [0, E) are the zero rows the gate/up kernel wrote, and enter the sum as zeros, as they do in MoeCombine.
+__global__ __launch_bounds__(256) void reduce_combine_kernel(const float* __restrict__ partial,
+                                                             const int32_t* __restrict__ slot_row,
+                                                             const int32_t* __restrict__ ids,
+                                                             const uint16_t* __restrict__ weights, int E, int T,
+                                                             int K, int H, int nsplit, uint16_t* __restrict__ expert_out,
+                                                             uint16_t* __restrict__ y) {
+#pragma clang fp contract(off)
+    const int vec = H / 8;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (idx >= static_cast<int64_t>(T) * vec) return;
+    const int t = static_cast<int>(idx / vec);
+    const int c = static_cast<int>(idx % vec) * 8;
+    const size_t total_rows = static_cast<size_t>(T) * K;
+    float yacc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) yacc[j] = 0.0f;
+    for (int k = 0; k < K; ++k) {
+        const int sl = t * K + k;
+        const int id = ids[sl];
+        f16x8 o;
+        if (id >= 0 && id < E) {
+            const float* src = partial + static_cast<size_t>(slot_row[sl]) * H + c;
+            float acc[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[j] = src[j];
+            for (int s = 1; s < nsplit; ++s) {
+                const float* ps = src + static_cast<size_t>(s) * total_rows * H;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[j] += ps[j];
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o[j] = static_cast<f16>(acc[j]);
+            *reinterpret_cast<f16x8*>(expert_out + static_cast<size_t>(sl) * H + c) = o;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o[j] = static_cast<f16>(0.0f);
+        }
+        const float w = f16_bits_to_f32(weights[sl]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) yacc[j] = yacc[j] + w * static_cast<float>(o[j]);
+    }
+    f16x8 out;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) out[j] = static_cast<f16>(yacc[j]);
+    *reinterpret_cast<f16x8*>(y + static_cast<size_t>(t) * H + c) = out;
+}
+
 // K-range for one workgroup: the largest multiple of 32*D dividing kdim such that rows_cap rows of it (padded)
 // fit the LDS; deepest ring first. Sets kc, D, rows_cap.
 struct StreamShape {
@@ -536,13 +592,14 @@ int stream_down_grid(int E, int H, int I) {
 
 hipError_t launch_ffn_stream(const uint16_t* x, const int32_t* expert_ids, const uint16_t* expert_weights,
                              uint16_t* expert_out, const FfnWorkspace& ws, int T, int H, int E, int K, int I,
-                             hipStream_t stream) {
+                             hipStream_t stream, const uint16_t* weights, uint16_t* y) {
     StreamArgs p{};
     p.sorted_slot = ws.sorted_slot;
     p.ids = expert_ids;
     p.S = T * K;
     p.offsets_out = ws.offsets;
     p.sorted_out = ws.sorted_slot;
+    p.slot_row_out = ws.slot_row;
     p.expert_out = expert_out;
     p.offsets = ws.offsets;
     p.w = expert_weights;
@@ -587,8 +644,14 @@ hipError_t launch_ffn_stream(const uint16_t* x, const int32_t* expert_ids, const
         err = dn.nsplit > 1 ? launch_stream_epi<kPartial>(p, dn.d, stream_down_grid(E, H, I), stream)
                             : launch_stream_epi<kScatter>(p, dn.d, stream_down_grid(E, H, I), stream);
     }
-    if (err != hipSuccess || dn.nsplit <= 1) return err;
-    {
+    if (err != hipSuccess) return err;
+    if (dn.nsplit <= 1) return y ? launch_combine(expert_out, weights, y, T, H, K, stream) : hipSuccess;
+    if (y) {
+        TraceScope trace("moe_ffn_down_reduce_combine", stream);
+        const int64_t work = static_cast<int64_t>(T) * (H / 8);
+        reduce_combine_kernel<<<static_cast<int>((work + 255) / 256), 256, 0, stream>>>(
+            ws.partial, ws.slot_row, expert_ids, weights, E, T, K, H, dn.nsplit, expert_out, y);
+    } else {
         TraceScope trace("moe_ffn_down_reduce", stream);
         const int64_t work = static_cast<int64_t>(T) * K * (H / 8);
         down_reduce_kernel<<<static_cast<int>((work + 255) / 256), 256, 0, stream>>>(

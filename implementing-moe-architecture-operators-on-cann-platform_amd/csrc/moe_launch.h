@@ -43,6 +43,7 @@ struct FfnWorkspace {
     int32_t* sorted_slot;  // [T*K]   slot index t*K + k of each sorted row, experts ascending, slots ascending
     uint16_t* hidden;      // [T*K, I] fp16 SwiGLU intermediate, rows in sorted order
     float* partial;        // [nsplit, T*K, H] fp32 split-K partial sums of the down projection (may be empty)
+    int32_t* slot_row;     // [T*K]   sorted row of each slot with a valid id (weight-streaming schedule only)
 };
 size_t ffn_workspace_bytes(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I);
 FfnWorkspace ffn_workspace_carve(void* base, int64_t T, int64_t H, int64_t E, int64_t K, int64_t I);
@@ -66,9 +67,11 @@ bool stream_supported(int H, int I);
 size_t stream_partial_bytes(int T, int H, int K, int I);
 int stream_gateup_grid(int E, int H, int I);
 int stream_down_grid(int E, int H, int I);
+// with y non-null (and weights) the combine is produced too: by the split reduce when the down projection is
+// split over K, else by the combine kernel after the FFN
 hipError_t launch_ffn_stream(const uint16_t* x, const int32_t* expert_ids, const uint16_t* expert_weights,
                              uint16_t* expert_out, const FfnWorkspace& ws, int T, int H, int E, int K, int I,
-                             hipStream_t stream);
+                             hipStream_t stream, const uint16_t* weights = nullptr, uint16_t* y = nullptr);
 // LDS-tiled schedule (moe_ffn_tiled.hip)
 bool tiled_supported(int H, int I);
 int tiled_block_threads();
@@ -82,6 +85,10 @@ int ffn_schedule(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I);
 // the whole FFN: permute (tiled schedule; the streaming schedule finds rows itself) and the two GEMMs
 hipError_t launch_ffn(const uint16_t* x, const int32_t* expert_ids, const uint16_t* expert_weights,
                       uint16_t* expert_out, FfnWorkspace ws, int T, int H, int E, int K, int I, hipStream_t stream);
+// the FFN followed by the combine: expert_out as launch_ffn writes it, y as launch_combine would compute it
+hipError_t launch_ffn_combine(const uint16_t* x, const int32_t* expert_ids, const uint16_t* weights,
+                              const uint16_t* expert_weights, uint16_t* expert_out, uint16_t* y, FfnWorkspace ws,
+                              int T, int H, int E, int K, int I, hipStream_t stream);
 
 // ---- combine (moe_combine.hip) ----
 int combine_block_threads();

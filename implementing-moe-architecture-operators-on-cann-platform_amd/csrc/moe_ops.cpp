@@ -253,6 +253,35 @@ moe_status moe_expert_ffn(const uint16_t* x, const int32_t* expert_ids, const ui
     return ok();
 }
 
+// MoeExpertFFN + MoeCombine in one call (optional fast path; both operators stay the contract)
+moe_status moe_expert_ffn_combine(const uint16_t* x, const int32_t* expert_ids, const uint16_t* weights,
+                                  const uint16_t* expert_weights, uint16_t* expert_out, uint16_t* y,
+                                  void* workspace, size_t workspace_bytes, int64_t T, int64_t H, int64_t E, int64_t K,
+                                  int64_t I, void* stream) {
+    moe_status st = check_ffn_sizes(T, H, E, K, I);
+    if (st != MOE_OK) return st;
+    st = check_combine_sizes(T, H, K);
+    if (st != MOE_OK) return st;
+    if (T == 0) return ok();
+    if (!x || !expert_ids || !weights || !expert_weights || !expert_out || !y)
+        return fail(MOE_ERR_NULL, "MoeExpertFFN+MoeCombine: null tensor pointer");
+    const size_t need = moe::ffn_workspace_bytes(T, H, E, K, I);
+    if (!workspace || workspace_bytes < need)
+        return fail(MOE_ERR_WORKSPACE, "MoeExpertFFN+MoeCombine: workspace %zu bytes at %p, need %zu", workspace_bytes,
+                    workspace, need);
+    if (!aligned16(x) || !aligned16(expert_weights) || !aligned16(expert_out) || !aligned16(workspace) ||
+        !aligned16(y))
+        return fail(MOE_ERR_UNSUPPORTED,
+                    "MoeExpertFFN+MoeCombine: x, expert_weights, expert_out, y, workspace must be 16-byte aligned");
+    const hipStream_t s = as_stream(stream);
+    const moe::FfnWorkspace ws = moe::ffn_workspace_carve(workspace, T, H, E, K, I);
+    const hipError_t err = moe::launch_ffn_combine(x, expert_ids, weights, expert_weights, expert_out, y, ws,
+                                                   static_cast<int>(T), static_cast<int>(H), static_cast<int>(E),
+                                                   static_cast<int>(K), static_cast<int>(I), s);
+    if (err != hipSuccess) return hip_fail(err, "MoeExpertFFN+MoeCombine launch");
+    return ok();
+}
+
 // ------------------------------------------------------------------------------------------------
 // MoeCombine
 // ------------------------------------------------------------------------------------------------

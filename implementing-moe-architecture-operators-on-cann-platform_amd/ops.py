@@ -128,6 +128,33 @@ def MoeCombine(expert_out: torch.Tensor, expert_ids: torch.Tensor | None, weight
     return y
 
 
+def MoeExpertFFNCombine(x: torch.Tensor, expert_ids: torch.Tensor, weights: torch.Tensor,
+                        expert_weights: torch.Tensor, intermediateSize: int = 0,
+                        workspace: torch.Tensor | None = None, stream=None) -> tuple[torch.Tensor, torch.Tensor]:
+    """MoeExpertFFN then MoeCombine in one call (moe_expert_ffn_combine): -> (expert_out[T,K,H], y[T,H]), both
+    fp16, expert_out as MoeExpertFFN returns it and y bit-identical to MoeCombine(expert_out, ...)."""
+    _need(x, "x", torch.float16)
+    _need(expert_ids, "expert_ids", torch.int32)
+    _need(weights, "weights", torch.float16)
+    _need(expert_weights, "expert_weights", torch.float16)
+    out_shape, out_dt, inter = infer_expert_ffn(tuple(x.shape), tuple(expert_ids.shape),
+                                                tuple(expert_weights.shape), intermediateSize)
+    T, H = x.shape
+    E, K = expert_weights.shape[0], expert_ids.shape[1]
+    if tuple(weights.shape) != (T, K):
+        raise MoeError(3, f"weights shape {tuple(weights.shape)} != {(T, K)}")
+    need = workspace_bytes(T, H, E, K, inter)
+    if workspace is None:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
+    expert_out = torch.empty(out_shape, dtype=out_dt, device=x.device)
+    y = torch.empty((T, H), dtype=torch.float16, device=x.device)
+    check(_lib.load().moe_expert_ffn_combine(x.data_ptr(), expert_ids.data_ptr(), weights.data_ptr(),
+                                             expert_weights.data_ptr(), expert_out.data_ptr(), y.data_ptr(),
+                                             workspace.data_ptr(), workspace.numel() * workspace.element_size(), T,
+                                             H, E, K, inter, _stream_ptr(stream)))
+    return expert_out, y
+
+
 def moe_layer(x: torch.Tensor, w_gate: torch.Tensor, expert_weights: torch.Tensor, topK: int = 2,
               workspace: torch.Tensor | None = None, stream=None):
     """The three operators chained as the reference harness chains them (tests/test_moe.cpp:444-463).

@@ -117,7 +117,8 @@ moe_status moe_expert_ffn_infer_shape(const int64_t* x_dims, int32_t x_rank, con
 moe_status moe_expert_ffn_infer_dtype(moe_dtype* expert_out_dtype);
 
 /* Workspace bytes for one call (TilingFunc workspace, op_host/moe_ops.cpp:340-349). Holds the expert-sorted
- * slot order, per-expert offsets and the fp16 SwiGLU intermediate [T*K, I]. 0 for invalid sizes. */
+ * slot order, per-expert offsets and the fp16 SwiGLU intermediate [T*K, I]; on the weight-streaming schedule
+ * also the split-K partial sums and the slot -> sorted-row map. 0 for invalid sizes. */
 size_t moe_expert_ffn_workspace_bytes(int64_t num_tokens, int64_t hidden_size, int64_t num_experts,
                                       int64_t top_k, int64_t intermediate_size);
 
@@ -169,6 +170,20 @@ moe_status moe_combine_plan_for(int64_t num_tokens, int64_t hidden_size, int64_t
  * expert_ids may be NULL. */
 moe_status moe_combine(const uint16_t* expert_out, const int32_t* expert_ids, const uint16_t* weights, uint16_t* y,
                        int64_t num_tokens, int64_t hidden_size, int64_t top_k, void* stream);
+
+/* ------------------------------------------------------------------------------------------------------
+ * Optional fast path: MoeExpertFFN followed by MoeCombine in one call. It has no single counterpart in the
+ * reference; it chains the kernel entries MoeExpertFFN (op_kernel/moe_expert_ffn.cpp:613-621) and MoeCombine
+ * (op_kernel/moe_combine.cpp:136-143), which stay the contract. expert_out is written exactly as
+ * moe_expert_ffn writes it, and y is bit-identical to moe_combine(expert_out, expert_ids, weights, y, ...).
+ * When the weight-streaming schedule splits the down projection over K, the split reduce produces y as well,
+ * saving the combine pass over expert_out; otherwise the combine kernel runs after the FFN. Deterministic (no
+ * atomics). Workspace as for moe_expert_ffn. Sizes and errors as moe_expert_ffn plus moe_combine's checks.
+ * ---------------------------------------------------------------------------------------------------- */
+moe_status moe_expert_ffn_combine(const uint16_t* x, const int32_t* expert_ids, const uint16_t* weights,
+                                  const uint16_t* expert_weights, uint16_t* expert_out, uint16_t* y,
+                                  void* workspace, size_t workspace_bytes, int64_t num_tokens, int64_t hidden_size,
+                                  int64_t num_experts, int64_t top_k, int64_t intermediate_size, void* stream);
 
 #ifdef __cplusplus
 }

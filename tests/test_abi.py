@@ -110,8 +110,8 @@ def test_plans(lib):
     ws = lib.moe_expert_ffn_workspace_bytes(128, 2048, 16, 2, 8192)
     assert fp.workspace_bytes == ws
     # offsets + sorted slots + the fp16 [T*K, I] intermediate + fp32 split-K partials of the down projection
-    # (I = 8192 is split into 4 K-ranges of 2048), each 256-byte aligned
-    assert ws == 256 + 1024 + 128 * 2 * 8192 * 2 + 4 * 128 * 2 * 2048 * 4
+    # (I = 8192 is split into 4 K-ranges of 2048) + the slot -> sorted-row map, each 256-byte aligned
+    assert ws == 256 + 1024 + 128 * 2 * 8192 * 2 + 4 * 128 * 2 * 2048 * 4 + 1024
     assert fp.permute_grid == 16 and fp.gateup_grid > 0 and fp.down_grid > 0
     assert lib.moe_expert_ffn_workspace_bytes(128, 2048, 16, 2, 8200) == 0  # I % 32 != 0
     assert lib.moe_expert_ffn_plan(16384, 2048, 64, 6, 1408, C.byref(fp)) == MOE_OK
@@ -137,6 +137,14 @@ def test_launch_argument_errors_return_before_launch(lib):
     assert lib.moe_expert_ffn(None, FAKE, FAKE, FAKE, FAKE, FAKE, need, *args) == ERR_NULL
     assert lib.moe_expert_ffn(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, need, 4, 64, 4, 5, 256, None) == ERR_ARG
     assert lib.moe_expert_ffn(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, need, 4, 64, 4, 2, 0, None) == ERR_ARG
+    # the fused FFN + combine checks both operators' rules before any launch
+    fused = lib.moe_expert_ffn_combine
+    assert fused(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, need - 1, *args) == ERR_WS
+    assert fused(FAKE, FAKE, FAKE, FAKE, FAKE, None, FAKE, need, *args) == ERR_NULL  # y
+    assert fused(FAKE, FAKE, None, FAKE, FAKE, FAKE, FAKE, need, *args) == ERR_NULL  # weights: used here
+    assert fused(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE + 2, FAKE, need, *args) == ERR_UNSUP  # misaligned y
+    assert fused(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, need, 4, 64, 4, 5, 256, None) == ERR_ARG
+    assert fused(None, None, None, None, None, None, None, 0, 0, 64, 4, 2, 256, None) == MOE_OK  # T = 0
     assert lib.moe_combine(None, None, None, None, 4, 64, 2, None) == ERR_NULL
     assert lib.moe_combine(FAKE, None, FAKE, FAKE, 4, 60, 2, None) == ERR_UNSUP
     assert lib.moe_combine(FAKE, None, FAKE, FAKE, 4, 64, 0, None) == ERR_ARG

@@ -282,6 +282,48 @@ def test_ffn_streaming_schedule_edges(ops, T, H, E, K, I, pattern):
     within(oracle.compare(eo[valid], eo_o[valid]), max_abs=1e-2, mean_abs=1e-3, cos=0.9999)
 
 
+@pytest.mark.parametrize("T,H,E,K,I,split", [
+    (64, 256, 8, 2, 512, 1),       # weight streaming, down in one K-range: FFN then the combine kernel
+    (40, 512, 4, 2, 2560, 2),      # weight streaming, down over 2 K-ranges: the split reduce also combines
+    (37, 128, 64, 3, 160, 1),      # ids outside [0, E): zero expert_out rows enter y as zeros
+    (300, 128, 4, 2, 128, 0),      # LDS-tiled schedule
+])
+def test_ffn_combine_fused_matches_separate(ops, T, H, E, K, I, split):
+    """moe_expert_ffn_combine: expert_out bit-identical to MoeExpertFFN, y bit-identical to MoeCombine on it."""
+    rng = np.random.default_rng(T * 7 + I)
+    x = rng.standard_normal((T, H)).astype(np.float16)
+    ew = np.concatenate([rng.standard_normal((E, 2 * I, H)) / math.sqrt(H),
+                         rng.standard_normal((E, I, H)) / math.sqrt(I)], axis=1).astype(np.float16)
+    ids = rng.integers(0, E, (T, K)).astype(np.int32)
+    if split == 1 and E == 64:
+        ids[3, 1], ids[9, 0], ids[20, 2] = -1, E, 1000
+    w = rng.uniform(0.05, 1.0, (T, K)).astype(np.float16)
+    log(f"[ffn+combine] T={T} H={H} E={E} K={K} I={I} schedule={ffn_schedule(T, H, E, K, I)}")
+    x_d, ids_d, w_d, ew_d = dev(x), dev(ids), dev(w), dev(ew)
+    eo_ref, _ = run_ffn(ops, x_d, ids_d, w_d, ew_d, I)
+    y_ref = ops.MoeCombine(eo_ref, ids_d, w_d, K)
+    eo, y = ops.MoeExpertFFNCombine(x_d, ids_d, w_d, ew_d, I)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(eo).view(np.uint16), host(eo_ref).view(np.uint16))
+    assert np.array_equal(host(y).view(np.uint16), host(y_ref).view(np.uint16))
+    # and y against the oracle's combine of that expert_out (fp32, k ascending), bit-exact
+    y_o = oracle.combine(f32(host(eo)), f32(w)).astype(np.float16)
+    assert np.array_equal(host(y).view(np.uint16), y_o.view(np.uint16))
+
+
+def test_ffn_combine_fused_decode_shape(ops):
+    """The decode layer's shape (down split over 4 K-ranges): fused y and expert_out equal the three-op path."""
+    cfg = synth.CONFIGS["decode"]
+    x_d, wg_d, ew_d = gpu_inputs(ops, cfg, 45)
+    ids_d, w_d = ops.MoeRoutingTopK(x_d, wg_d, cfg.K)
+    eo_ref, _ = run_ffn(ops, x_d, ids_d, w_d, ew_d, cfg.I)
+    y_ref = ops.MoeCombine(eo_ref, ids_d, w_d, cfg.K)
+    eo, y = ops.MoeExpertFFNCombine(x_d, ids_d, w_d, ew_d, cfg.I)
+    torch.cuda.synchronize()
+    assert torch.equal(eo.view(torch.int16), eo_ref.view(torch.int16))
+    assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16))
+
+
 def test_ffn_rejects_bad_workspace(ops):
     x = dev(np.zeros((4, 64), np.float16))
     ids = dev(np.zeros((4, 2), np.int32))
