@@ -431,6 +431,8 @@ def ffn_schedule(T, H, E, K, I) -> int:
     (257, 320, 3, 2, 192),    # partial n-tiles in both GEMMs (I = 192 -> 2 x 128, H = 320 -> 2 x 256)
     (600, 64, 8, 3, 64),      # K = 3, single k-stage
     (700, 192, 2, 1, 1408),   # >256 rows per expert (several m-tiles), DeepSeek's I
+    (8200, 64, 256, 2, 64),   # E = 256: the permute re-reads expert_ids instead of its LDS byte copy
+    (900, 64, 8, 2, 64),      # ids outside [0, E) through the permute's LDS byte copy (sentinel 255)
 ])
 def test_ffn_tiled_schedule_full_oracle(ops, T, H, E, K, I):
     assert ffn_schedule(T, H, E, K, I) == 1
@@ -439,12 +441,17 @@ def test_ffn_tiled_schedule_full_oracle(ops, T, H, E, K, I):
     ew = np.concatenate([rng.standard_normal((E, 2 * I, H)) / math.sqrt(H),
                          rng.standard_normal((E, I, H)) / math.sqrt(I)], axis=1).astype(np.float16)
     ids = np.stack([rng.permutation(E)[:K] for _ in range(T)]).astype(np.int32)
+    valid = np.ones((T, K), bool)
+    if T == 900:
+        ids[5, 0], ids[77, 1], ids[600, 0], ids[899, 1] = -1, E, 255, 1 << 20
+        valid = (ids >= 0) & (ids < E)
     w = np.full((T, K), 1.0 / K, np.float16)
     eo_d, ws = run_ffn(ops, dev(x), dev(ids), dev(w), dev(ew), I)
     check_permute(host(ws), ids, E)
     eo = f32(host(eo_d))
-    eo_o = oracle.expert_ffn(f32(x), ids, f32(ew), I)
-    m = oracle.compare(eo, eo_o)
+    assert not eo[~valid].any()
+    eo_o = oracle.expert_ffn(f32(x), np.where(valid, ids, 0), f32(ew), I)
+    m = oracle.compare(eo[valid], eo_o[valid])
     log(f"[tiled T{T} H{H} E{E} K{K} I{I}] expert_out vs oracle: {m}")
     within(m, max_abs=1e-2, mean_abs=1e-3, cos=0.9999)
 
