@@ -7,7 +7,7 @@ T=128, H=2048, E=16, K=2, I=8192 (fp16 I/O, fp32 accumulation) by default.
 A step is one pass of the layer over one batch of synthetic input resident in HBM: routing, the expert FFN
 (permute + fused gate/up/SwiGLU grouped GEMM + down grouped GEMM with the expert_out scatter) and combine, all
 through the C ABI of libmoe_mi355x.so on one stream, with caller-owned buffers allocated once.
-W warm-up steps, then four timed passes of K steps each, every pass between torch.cuda.synchronize() calls:
+W warm-up steps, then five timed passes of K steps each, every pass between torch.cuda.synchronize() calls:
   1. eager: the three C-ABI calls per step, nothing else recorded -> `value` and `ms_per_step`;
   2. graph replay: the same three calls captured once in a HIP graph, replayed K times (y checked bit-exact
      against the eager y first) -> `layer_us_graph_replay`;
@@ -16,6 +16,12 @@ W warm-up steps, then four timed passes of K steps each, every pass between torc
   4. fused: routing, then moe_expert_ffn_combine (the FFN and the combine in one call, an optional fast path;
      expert_out and y checked bit-exact against the three-operator layer first) -> `layer_us_fused_ffn_combine`.
      `value` stays the three-operator layer, the drop-in pipeline.
+  5. per-step events: the three-operator layer with an event pair around every step ->
+     `layer_us_per_step_events` (p10 / p50 / p90).
+Then two library kernels over 1 GiB give this box's achievable HBM rates next to the published 8 TB/s the
+roofline uses: a whole-line non-temporal streaming read (`hbm_read_gbps`, the access the decode weight stream
+uses) and a plain copy (`hbm_copy_gbps`, read + write). Kernels whose per-launch inputs fit the 256 MB Infinity
+Cache (routing and combine at decode) are flagged `cache_resident`: repeated steps read them from it.
 
 The JSON line also carries:
   roofline      the dominant kernel's algorithmic bytes (or flops) per launch / its average event-timed
@@ -45,6 +51,7 @@ PKG = "implementing-moe-architecture-operators-on-cann-platform_amd"
 METRIC = "MoE layer µs; FFN TFLOPS & HBM GB/s (% peak) at T=128,H=2048,E=16,I=8192"
 HBM_PEAK_GBS = 8000.0
 MFMA_FP16_PEAK_TFLOPS = 2500.0
+MALL_BYTES = 256 << 20  # MI355X Infinity Cache
 RIDGE = MFMA_FP16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
 
 
@@ -125,6 +132,7 @@ def main() -> int:
     ap.add_argument("--cpu-target-gflop", type=float, default=30.0,
                     help="size of the CPU baseline sample in GFLOP of expert FFN work")
     ap.add_argument("--no-graph", action="store_true", help="skip the HIP-graph replay timing")
+    ap.add_argument("--no-copy-rate", action="store_true", help="skip the 1 GiB read and copy rate measurements")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="instead of the layer, run moe_copy_bytes over MIB MiB (reference for HBM byte counters)")
     args = ap.parse_args()
@@ -229,6 +237,41 @@ def main() -> int:
         raise RuntimeError("the fused FFN + combine differs from the three-operator layer")
     fused_ms, fused_gpu_ms = timed(step_fused)
     progress(f"fused FFN + combine: {fused_ms * 1e3:.1f} us/step (host clock), {fused_gpu_ms * 1e3:.1f} us/step (events)")
+    # 5) per-step spread of the three-operator layer: an event pair around every step
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    for a, b in evs:
+        a.record(stream)
+        step()
+        b.record(stream)
+    torch.cuda.synchronize()
+    per_step_us = np.array([a.elapsed_time(b) * 1e3 for a, b in evs])
+    spread = {q: round(float(np.percentile(per_step_us, p)), 2) for q, p in (("p10", 10), ("p50", 50), ("p90", 90))}
+    progress(f"per-step events: p10 {spread['p10']} / p50 {spread['p50']} / p90 {spread['p90']} us")
+    # 6) achievable HBM rate on this box: the library's plain copy kernel over 1 GiB (read + write)
+    copy_gbps = read_gbps = None
+    if not args.no_copy_rate:
+        nb = 1 << 30
+        src = torch.empty(nb, dtype=torch.uint8, device=dev)
+        dst = torch.empty(nb, dtype=torch.uint8, device=dev)
+        src.fill_(1)
+        ops.copy_bytes_(dst, src)
+        with ops.kernel_trace() as ck:
+            for _ in range(5):
+                ops.copy_bytes_(dst, src)
+            torch.cuda.synchronize()
+        (_, (nl, tot_ms)), = ck.items()
+        copy_gbps = round(2 * nb / (tot_ms / nl * 1e-3) / 1e9, 1)
+        del dst
+        ops.stream_read_(src)
+        with ops.kernel_trace() as rk:
+            for _ in range(5):
+                ops.stream_read_(src)
+            torch.cuda.synchronize()
+        (_, (nl, tot_ms)), = rk.items()
+        read_gbps = round(nb / (tot_ms / nl * 1e-3) / 1e9, 1)
+        del src
+        progress(f"1 GiB: copy kernel {copy_gbps} GB/s (read + write), streaming read {read_gbps} GB/s")
 
     ids_h = ids.cpu().numpy()
     active = int((np.bincount(ids_h.ravel(), minlength=E) > 0).sum())
@@ -239,7 +282,9 @@ def main() -> int:
         b, f = work.get(name, (0, 0))
         per_kernel[name] = {"launches": launches, "avg_us": round(avg * 1e3, 2),
                             "GB/s": round(b / (avg * 1e-3) / 1e9, 1) if b else None,
-                            "TFLOP/s": round(f / (avg * 1e-3) / 1e12, 2) if f else None}
+                            "TFLOP/s": round(f / (avg * 1e-3) / 1e12, 2) if f else None,
+                            # inputs re-read every step that fit the 256 MB Infinity Cache are served from it
+                            "cache_resident": bool(b) and b < MALL_BYTES}
     ffn_names = ("moe_permute", "moe_ffn_gateup_swiglu", "moe_ffn_down", "moe_ffn_down_reduce")
     ffn_ms = sum(kernels[n][1] / kernels[n][0] for n in ffn_names if n in kernels)
     ffn_flops = 6 * T * K * H * I
@@ -306,12 +351,15 @@ def main() -> int:
         "layer_us_graph_replay": round(graph_ms * 1e3, 2) if graph_ms else None,
         "layer_us_traced": round(traced_ms * 1e3, 2),
         "layer_us_fused_ffn_combine": round(fused_ms * 1e3, 2),
+        "layer_us_per_step_events": spread,
         "ffn_us": round(ffn_ms * 1e3, 2),
         "ffn_tflops": round(ffn_flops / (ffn_ms * 1e-3) / 1e12, 2),
         "ffn_hbm_gbps": round(ffn_bytes / (ffn_ms * 1e-3) / 1e9, 1),
         "ffn_hbm_frac": round(ffn_bytes / (ffn_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "ffn_mfma_frac": round(ffn_flops / (ffn_ms * 1e-3) / 1e12 / MFMA_FP16_PEAK_TFLOPS, 4),
         "kernels": per_kernel,
+        "hbm_copy_gbps": copy_gbps,
+        "hbm_read_gbps": read_gbps,
         "roofline": roofline,
         "cpu_baseline": cpu_baseline,
         "cpu_baseline_tiled": cpu_baseline_tiled,

@@ -78,6 +78,7 @@ SIGNATURES = {
     "moe_synth_normal_f16": (_I32, [_P, C.c_uint64, C.c_uint64, C.c_uint64, C.c_double, C.c_double,
                                     C.c_uint64, C.c_uint64, _P]),
     "moe_copy_bytes": (_I32, [_P, _P, C.c_uint64, _P]),
+    "moe_stream_read_bytes": (_I32, [_P, C.c_uint64, _P]),
 }
 
 _lock = threading.Lock()

@@ -101,5 +101,6 @@ hipError_t launch_combine(const uint16_t* expert_out, const uint16_t* weights, u
 hipError_t launch_synth_normal_f16(uint16_t* out, uint64_t n, uint64_t seed, uint64_t stream_id, double sigma_a,
                                    double sigma_b, uint64_t period, uint64_t split, hipStream_t stream);
 hipError_t launch_copy_bytes(void* dst, const void* src, uint64_t bytes, hipStream_t stream);
+hipError_t launch_stream_read(const void* src, uint64_t bytes, hipStream_t stream);
 
 }  // namespace moe

@@ -363,4 +363,14 @@ moe_status moe_copy_bytes(void* dst, const void* src, uint64_t bytes, void* stre
     return ok();
 }
 
+moe_status moe_stream_read_bytes(const void* src, uint64_t bytes, void* stream) {
+    if (bytes == 0) return ok();
+    if (!src) return fail(MOE_ERR_NULL, "moe_stream_read_bytes: null pointer");
+    if (bytes % 16384 != 0 || !aligned16(src))
+        return fail(MOE_ERR_ARG, "moe_stream_read_bytes: size must be a multiple of 16384, pointer 16-byte aligned");
+    hipError_t err = moe::launch_stream_read(src, bytes, as_stream(stream));
+    if (err != hipSuccess) return hip_fail(err, "moe_stream_read_bytes launch");
+    return ok();
+}
+
 }  // extern "C"

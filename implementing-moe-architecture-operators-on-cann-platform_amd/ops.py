@@ -181,6 +181,12 @@ def copy_bytes_(dst: torch.Tensor, src: torch.Tensor, stream=None) -> None:
     check(_lib.load().moe_copy_bytes(dst.data_ptr(), src.data_ptr(), n, _stream_ptr(stream)))
 
 
+def stream_read_(src: torch.Tensor, stream=None) -> None:
+    """Read a device tensor (size a multiple of 16 KiB) with moe_stream_read_bytes: achievable HBM read rate."""
+    n = src.numel() * src.element_size()
+    check(_lib.load().moe_stream_read_bytes(src.data_ptr(), n, _stream_ptr(stream)))
+
+
 @contextlib.contextmanager
 def kernel_trace():
     """Record HIP events around every kernel the library launches; yields a dict filled on exit with

@@ -32,6 +32,10 @@ moe_status moe_synth_normal_f16(uint16_t* out, uint64_t n, uint64_t seed, uint64
 /* Plain device copy of `bytes` bytes (multiple of 16, 16-byte aligned) used to calibrate HBM counters. */
 moe_status moe_copy_bytes(void* dst, const void* src, uint64_t bytes, void* stream);
 
+/* Read `bytes` bytes (multiple of 16384, 16-byte aligned) with whole-line non-temporal loads and discard them:
+ * the achievable HBM read rate of this device, reported beside the published peak. */
+moe_status moe_stream_read_bytes(const void* src, uint64_t bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

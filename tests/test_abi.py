@@ -150,6 +150,8 @@ def test_launch_argument_errors_return_before_launch(lib):
     assert lib.moe_combine(FAKE, None, FAKE, FAKE, 4, 64, 0, None) == ERR_ARG
     assert lib.moe_synth_normal_f16(None, 10, 0, 0, 1.0, 1.0, 1, 1, None) == ERR_NULL
     assert lib.moe_copy_bytes(FAKE, FAKE, 17, None) == ERR_ARG
+    assert lib.moe_stream_read_bytes(None, 16384, None) == ERR_NULL
+    assert lib.moe_stream_read_bytes(FAKE, 16000, None) == ERR_ARG
 
 
 def test_last_error_is_cleared_on_success(lib):
