@@ -323,13 +323,24 @@ __global__ __launch_bounds__(kThreads) void ffn_stream_kernel(StreamArgs p, int 
     const int gpr = p.kc / 8;
     const int stride = p.kc + 8;
 
-    if (EPI == kSwiGLU && blockIdx.x == 0) {
-        // once per call: zero the expert_out rows of invalid ids (they belong to no expert)
-        for (int sl = tid; sl < p.S; sl += kThreads) {
-            const int id = p.ids[sl];
-            if (id >= 0 && id < p.E) continue;
-            u32x4* dst = reinterpret_cast<u32x4*>(p.expert_out + static_cast<size_t>(sl) * p.H);
-            for (int j = 0; j < p.H / 8; ++j) dst[j] = u32x4{0u, 0u, 0u, 0u};
+    if (EPI == kSwiGLU) {
+        // once per call: zero the expert_out rows of ids outside [0, E) (they belong to no expert); workgroup b
+        // takes slots [b * per, (b + 1) * per), 4 id loads in flight per thread
+        const int per = (p.S + static_cast<int>(gridDim.x) - 1) / static_cast<int>(gridDim.x);
+        const int s_beg = min(p.S, static_cast<int>(blockIdx.x) * per), s_end = min(p.S, s_beg + per);
+        for (int base = s_beg; base < s_end; base += 4 * kThreads) {
+            int id[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int sl = base + t * kThreads + tid;
+                id[t] = sl < s_end ? p.ids[sl] : 0;
+            }
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                if (id[t] >= 0 && id[t] < p.E) continue;
+                u32x4* dst = reinterpret_cast<u32x4*>(p.expert_out + static_cast<size_t>(base + t * kThreads + tid) * p.H);
+                for (int j = 0; j < p.H / 8; ++j) dst[j] = u32x4{0u, 0u, 0u, 0u};
+            }
         }
     }
 
@@ -369,6 +380,7 @@ __global__ __launch_bounds__(kThreads) void ffn_stream_kernel(StreamArgs p, int 
         const bool active = n0 < p.ndim;
         const int k0 = split * p.kc;
         const size_t ebase = static_cast<size_t>(e) * 3 * static_cast<size_t>(p.I) * p.H;
+        // D == 1 ring: lane (row, kg) reads weight row n0 + row, k-group kg of each k-step
         const uint16_t* w0 =
             p.w + ebase + p.w_off + static_cast<size_t>(active ? n0 + row : row) * p.kdim + k0 + kg * 8;
         const uint16_t* w1 = w0 + p.w1_off;
@@ -376,6 +388,7 @@ __global__ __launch_bounds__(kThreads) void ffn_stream_kernel(StreamArgs p, int 
 
         constexpr int CB = D / 2;  // column blocks in flight (full-line ring, D >= 2)
         constexpr int CBn = CB > 0 ? CB : 1;
+        // D >= 2 ring: lane reads 16 B chunk lane % 8 of weight rows n0 + lane / 8 (+ 8) of each column block
         const uint16_t* wbase = p.w + ebase + p.w_off + static_cast<size_t>(active ? n0 : 0) * p.kdim + k0 +
                                 static_cast<size_t>(lane >> 3) * p.kdim + (lane & 7) * 8;
         const uint16_t* const wr[4] = {wbase, wbase + static_cast<size_t>(8) * p.kdim, wbase + p.w1_off,
@@ -383,10 +396,10 @@ __global__ __launch_bounds__(kThreads) void ffn_stream_kernel(StreamArgs p, int 
 
         for (int mc = 0; mc < ne; mc += p.rows_cap) {
             const int rows = min(p.rows_cap, ne - mc);
-            f16x8 r0[D], r1[D];
-            f16x8 rg[CBn][4];
+            f16x8 rg[CBn][4];   // D >= 2: whole-line ring (wr, column blocks)
+            f16x8 r0[D], r1[D];  // D == 1: loads straight into the MFMA order (w0, w1, k-steps)
             if (active) {
-                if (CB > 0) {
+                if constexpr (CB > 0) {
                     line_prime<CBn>(wr, rot / 2, rg);
                 } else {
 #pragma unroll
@@ -428,7 +441,7 @@ __global__ __launch_bounds__(kThreads) void ffn_stream_kernel(StreamArgs p, int 
                 lds_barrier();
             }
             if (active) {
-                if (CB > 0) {
+                if constexpr (CB > 0) {
                     uint16_t* tb = lds + p.rows_cap * stride + wave * 1024;
                     if (rows > 16)
                         line_pass<2, CBn, EPI>(p, lds, tb, wr, rg, rot / 2, off, ne, mc, n0, split, lane);
@@ -441,7 +454,6 @@ __global__ __launch_bounds__(kThreads) void ffn_stream_kernel(StreamArgs p, int 
                 }
             }
         }
-
     }
 }
 
