@@ -43,6 +43,10 @@ __device__ __forceinline__ f32x4 mfma16x16x32(f16x8 a, f16x8 b, f32x4 c) {
 
 __device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x) & (kWave - 1); }
 
+// s_waitcnt immediate that waits until at most n (< 64) vector-memory operations of this wave are outstanding
+// (gfx9 encoding: vmcnt bits [3:0] and [15:14]; lgkmcnt and expcnt left at their maximum, i.e. not waited on).
+constexpr unsigned vmcnt_imm(int n) { return 0x0f70u | (n & 15) | ((n >> 4) << 14); }
+
 // SwiGLU of one fp32 (gate, up) pair: silu(g) * u = g / (1 + exp(-g)) * u. Contraction into FMAs is off, so each
 // operation rounds on its own and the result does not depend on how the compiler schedules the code around it
 // (with contraction on, unrolled copies of the same epilogue were seen to round differently).

@@ -13,8 +13,11 @@
 //                sub-tile (8 x 4 v_mfma_f32_16x16x32_f16 tiles, 128 fp32 accumulators per lane: with 256 per
 //                lane the accumulators plus the loop's other live values exceed one wave's register file and
 //                the compiler shuffles them between register files every iteration)
-//   pipeline     the next stage's 8 x 16 B per thread are loaded into registers while the current stage is
-//                multiplied out of LDS; two LDS stages, one barrier per stage
+//   pipeline     the next stage is copied straight from global memory into the other LDS buffer
+//                (global_load_lds_dwordx4: no staging registers, no LDS store instructions) while the current
+//                stage is multiplied; two LDS stages, one barrier per stage. The barrier carries no release
+//                fence: one would wait for the copies in flight (vmcnt(0)) before the MFMAs are done. 7-8 %
+//                faster than staging through registers.
 //   LDS layout   unpadded 128-byte rows of 8 granules of 16 B; granule g of row r is stored at g ^ ((r >> 1) & 7),
 //                so the 16 rows one ds_read_b128 touches (same logical granule) spread over all banks
 //   gate/up      the 256 weight rows of a tile are, per wave quarter, 32 W_gate rows and the matching 32 W_up
@@ -40,7 +43,8 @@ constexpr int kBK = 64;            // k per stage
 constexpr int kPitch = kBK;        // LDS row pitch in halfs (granules XOR-swizzled)
 constexpr int kThreads = 512;      // 8 waves
 constexpr int kStageHalfs = (kBM + kBN) * kPitch;
-constexpr int kLdsBytes = 2 * kStageHalfs * 2;  // 131072
+constexpr int kNStage = 2;
+constexpr int kLdsBytes = kNStage * kStageHalfs * 2;
 constexpr int kXcds = 8;
 
 enum Epilogue { kSwiGLU = 0, kScatter = 1 };
@@ -58,10 +62,14 @@ struct TiledArgs {
     int gather;                  // gate/up: activation row r -> x[sorted_slot[r] / K]
 };
 
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+// Barrier of the copy ring. The only LDS writes of the main loop are this wave's direct-to-LDS copies, which the
+// caller's explicit vmcnt wait covers, and every fragment read of the stage has fed an MFMA before the wave gets
+// here. A workgroup-scope release fence would also wait for the copies still in flight (vmcnt(0)).
+__device__ __forceinline__ void ring_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    __builtin_amdgcn_sched_barrier(0);
 }
 
 // Linear tile -> (expert, m-tile, n-tile); false when t is past the last tile.
@@ -99,70 +107,50 @@ __global__ __launch_bounds__(kThreads) void ffn_tiled_kernel(TiledArgs p) {
     if (!find_tile(p, t, &e, &mt, &nt, &off, &ne)) return;
 
     const int tid = static_cast<int>(threadIdx.x);
-    const int wave = tid / kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int lane = lane_id();
     const int row16 = lane & 15, kg = lane >> 4;
     const int wm = wave >> 2, wn = wave & 3;  // 2 x 4 waves: rows wm*128.., weight rows wn*64..
     const int m0 = mt * kBM;
     const size_t ebase = static_cast<size_t>(e) * 3 * static_cast<size_t>(p.I) * p.H;
 
-    // ---- per-thread global load plan: rows (tid / 8) + 64 j, k-granule tid % 8 (16 B) ----
-    // 32-bit element offsets from uniform bases keep the vector-register budget for the accumulators.
-    const int kgr = tid & 7;
-    const uint16_t* abase = p.act + kgr * 8;
-    const uint16_t* wbase = p.w + ebase + kgr * 8;
+    // direct-to-LDS plan: per stage and operand, wave w issues 4 instructions j, each filling 8 whole LDS rows
+    // r = (4 w + j) * 8 + lane / 8 (128 B each); lane fetches global granule (lane % 8) ^ ((r >> 1) & 7)
     uint32_t aoff[4], boff[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int r = (tid >> 3) + 64 * j;  // 0..255
+        const int r = (wave * 4 + j) * 8 + (lane / 8);
+        const int gq = (lane % 8) ^ ((r >> 1) & 7);
         const int m = min(m0 + r, ne - 1);
         const uint32_t src = p.gather ? static_cast<uint32_t>(p.sorted_slot[off + m] / p.K) : static_cast<uint32_t>(off + m);
-        aoff[j] = src * static_cast<uint32_t>(p.kdim);
+        aoff[j] = src * static_cast<uint32_t>(p.kdim) + gq * 8;
         if (EPI == kSwiGLU) {
-            // tile row r: wave quarter r/64; within it 32 gate rows then the 32 matching up rows
             const int quarter = r >> 6, sub = r & 63;
             const int ic = min(nt * 128 + quarter * 32 + (sub & 31), p.I - 1);
-            boff[j] = (sub < 32 ? 0u : static_cast<uint32_t>(p.I) * p.H) + static_cast<uint32_t>(ic) * p.H;
+            boff[j] = (sub < 32 ? 0u : static_cast<uint32_t>(p.I) * p.H) + static_cast<uint32_t>(ic) * p.H + gq * 8;
         } else {
             const int n = min(nt * kBN + r, p.H - 1);
-            boff[j] = 2u * static_cast<uint32_t>(p.I) * p.H + static_cast<uint32_t>(n) * p.I;
+            boff[j] = 2u * static_cast<uint32_t>(p.I) * p.H + static_cast<uint32_t>(n) * p.I + gq * 8;
         }
     }
+    const uint16_t* abase = p.act;
+    const uint16_t* wbase = p.w + ebase;
 
     f32x4 acc[8][4];
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    u32x4 ga[4], gb[4];
-    auto load_stage = [&](int ks) {
+    auto issue_stage = [&](int ks) {
         const int k0 = ks * kBK;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) ga[j] = *reinterpret_cast<const u32x4*>(abase + aoff[j] + k0);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) gb[j] = *reinterpret_cast<const u32x4*>(wbase + boff[j] + k0);
-    };
-    auto store_stage = [&](int buf) {
-        uint16_t* sa = lds + buf * kStageHalfs;
+        uint16_t* sa = lds + (ks % kNStage) * kStageHalfs;
         uint16_t* sb = sa + kBM * kPitch;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int r = (tid >> 3) + 64 * j;
-            const int pg = kgr ^ ((r >> 1) & 7);
-            *reinterpret_cast<u32x4*>(sa + r * kPitch + pg * 8) = ga[j];
-            *reinterpret_cast<u32x4*>(sb + r * kPitch + pg * 8) = gb[j];
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(abase + aoff[j] + k0),
+                                             (__attribute__((address_space(3))) void*)(sa + (wave * 4 + j) * 8 * kPitch), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(wbase + boff[j] + k0),
+                                             (__attribute__((address_space(3))) void*)(sb + (wave * 4 + j) * 8 * kPitch), 16, 0, 0);
         }
     };
-
-    const int nstages = p.kdim / kBK;
-    load_stage(0);
-    store_stage(0);
-    lds_barrier();
-    for (int s = 0; s < nstages; ++s) {
-        const int buf = s & 1;
-        if (s + 1 < nstages) load_stage(s + 1);
-        // row (16 i + row16) has swizzle ((row16 >> 1) & 7): the 16-row offsets leave it unchanged
+    auto mma_stage = [&](int ks, bool first) {
+        const int buf = ks % kNStage;
         const int sw = (row16 >> 1) & 7;
         const uint16_t* sa = lds + buf * kStageHalfs + (wm * 128 + row16) * kPitch;
         const uint16_t* sb = lds + buf * kStageHalfs + (kBM + wn * 64 + row16) * kPitch;
@@ -176,11 +164,31 @@ __global__ __launch_bounds__(kThreads) void ffn_tiled_kernel(TiledArgs p) {
             for (int j = 0; j < 4; ++j) {
                 const f16x8 bf = *reinterpret_cast<const f16x8*>(sb + j * 16 * kPitch + gran);
 #pragma unroll
-                for (int i = 0; i < 8; ++i) acc[i][j] = mfma16x16x32(af[i], bf, acc[i][j]);
+                for (int i = 0; i < 8; ++i)
+                    acc[i][j] = mfma16x16x32(af[i], bf, first && kk == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[i][j]);
             }
         }
-        if (s + 1 < nstages) store_stage(buf ^ 1);
-        lds_barrier();
+    };
+
+    // two LDS stages: stage s + 1 is copied into the other buffer while stage s is multiplied
+    const int nstages = p.kdim / kBK;
+    issue_stage(0);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // this wave's copies of stage 0 are in LDS
+    ring_barrier();                            // and every wave's
+    if (nstages > 1) issue_stage(1);
+    mma_stage(0, true);  // the accumulators start from an inline zero, so they are never VGPR-initialised
+    if (nstages > 1) {
+        __builtin_amdgcn_sched_barrier(0);  // keep the copy wait after every MFMA of the stage
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        ring_barrier();
+        for (int s = 1; s + 1 < nstages; ++s) {
+            issue_stage(s + 1);  // into the buffer stage s - 1 used: the barrier above ended its reads
+            mma_stage(s, false);
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+            ring_barrier();
+        }
+        mma_stage(nstages - 1, false);
     }
 
     // ---- epilogue: acc[i][j] lane holds D[m = 4*kg + r][n = row16] of sub-tile (i, j) ----
