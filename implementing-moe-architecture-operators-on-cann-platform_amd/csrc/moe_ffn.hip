@@ -26,7 +26,7 @@ constexpr int64_t kTiledMinRowsPerExpert = 64;
 
 int ffn_schedule(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
     const bool stream_ok = stream_supported(static_cast<int>(H), static_cast<int>(I));
-    const bool tiled_ok = tiled_supported(static_cast<int>(H), static_cast<int>(I));
+    const bool tiled_ok = tiled_supported(T, H, E, K, I);
     const bool many_rows = T * K >= kTiledMinRowsPerExpert * E;
     if (tiled_ok && (many_rows || !stream_ok)) return 1;
     if (stream_ok) return 0;

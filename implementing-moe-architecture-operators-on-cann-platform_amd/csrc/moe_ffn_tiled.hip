@@ -5,29 +5,34 @@
 //
 // With ~1000 rows per expert (T = 8192, K = 2, E = 16) the GEMMs have an arithmetic intensity of ~1500 flop/B
 // against HBM, far above the MFMA ridge. Both are "NT": activation rows and weight rows are contiguous along the
-// reduction dim k. Measured on MI355X with stripped copies of this kernel: its global loads alone take ~44% of
-// its time (12 TB/s from L2), its MFMAs alone ~32%, but LDS stores + fragment reads + MFMAs without any global
-// load already ~82%. Per 64-k stage a CU moves 256 KB through LDS against 2048 MFMA cycles per SIMD, and the two
-// overlap poorly: the LDS side, not the memory system, is what a faster schedule has to shrink.
+// reduction dim k.
 //   macro tile   256 activation rows x 256 weight rows x 64 k per stage; 8 waves (2 x 4), each a 128 x 64
-//                sub-tile (8 x 4 v_mfma_f32_16x16x32_f16 tiles, 128 fp32 accumulators per lane: with 256 per
-//                lane the accumulators plus the loop's other live values exceed one wave's register file and
-//                the compiler shuffles them between register files every iteration)
-//   pipeline     the next stage is copied straight from global memory into the other LDS buffer
-//                (global_load_lds_dwordx4: no staging registers, no LDS store instructions) while the current
-//                stage is multiplied; two LDS stages, one barrier per stage. The barrier carries no release
-//                fence: one would wait for the copies in flight (vmcnt(0)) before the MFMAs are done. 7-8 %
-//                faster than staging through registers.
+//                sub-tile (8 x 4 v_mfma_f32_16x16x32_f16 tiles, 128 fp32 accumulators per lane). The weight
+//                fragment is the MFMA's first operand, so each lane ends with 4 consecutive output columns of one
+//                row and the epilogue stores 8 bytes at a time.
+//   copies       each stage is copied from global memory straight into LDS (buffer_load ... lds: no staging
+//                registers, no LDS store instructions; 32-bit offsets against buffer resources whose range ends
+//                at the buffer, so a read past it returns zeros instead of faulting)
+//   ring         two LDS slots. Stage q's 64 MFMAs per wave run in four phases of 16; the LDS fragment reads a
+//                later phase needs are issued between the MFMAs of the phase before (sched_group_barrier), so
+//                both pipes stay busy. One barrier per stage, between the third and the fourth phase: by then
+//                the wave has read all of stage q, and stage q + 1 has landed, so the barrier publishes q + 1
+//                and frees q's slot for the copies of q + 2.
+//   persistent   (gate/up) one workgroup per CU walks its tiles back to back and the ring runs on across
+//                them: the copies of a tile's first two stages go out during the previous tile's last two.
+//                The tile table (per-expert tile prefix and row offsets) is built once per workgroup in LDS, so
+//                finding a tile is a short LDS binary search; the next tile's 256 sorted-slot entries are copied
+//                into LDS a tile ahead. The down projection has ~2 tiles per CU, where the hardware's own
+//                dispatch balances better, so it runs one workgroup per tile through the same kernel.
 //   LDS layout   unpadded 128-byte rows of 8 granules of 16 B; granule g of row r is stored at g ^ ((r >> 1) & 7),
 //                so the 16 rows one ds_read_b128 touches (same logical granule) spread over all banks
 //   gate/up      the 256 weight rows of a tile are, per wave quarter, 32 W_gate rows and the matching 32 W_up
-//                rows, so each wave holds gate and up of the same (row, i) and applies SwiGLU in registers,
-//                writing fp16 hidden rows
+//                rows, so each wave holds gate and up of the same (row, i) and applies SwiGLU in registers
+//                (hardware exp2 and reciprocal, ~1 ulp each), writing fp16 hidden rows
 //   down         weight rows are W_down rows (output columns); the epilogue writes expert_out[slot] directly
-//   scheduling   tiles are (expert, n-tile, m-tile) with m fastest, numbered from the per-expert row counts
-//                at run time; the grid is an upper bound and surplus workgroups exit. Workgroups are dispatched
-//                round-robin over the 8 XCDs, so the linear tile order is remapped to give each XCD a
-//                contiguous range: the m-tiles that share a weight tile then share that XCD's L2.
+//   scheduling   tiles are (expert, n-tile, m-tile) with m fastest. Workgroups are dispatched round-robin over
+//                the 8 XCDs; each XCD owns a contiguous range of tiles, so the m-tiles that share a weight tile
+//                share that XCD's L2.
 // Rows past an expert's count are clamped to its last row on load and masked on store.
 
 #include "moe_device.h"
@@ -44,7 +49,8 @@ constexpr int kPitch = kBK;        // LDS row pitch in halfs (granules XOR-swizz
 constexpr int kThreads = 512;      // 8 waves
 constexpr int kStageHalfs = (kBM + kBN) * kPitch;
 constexpr int kNStage = 2;
-constexpr int kLdsBytes = kNStage * kStageHalfs * 2;
+constexpr int kLdsBytes = kNStage * kStageHalfs * 2;  // the ring; the tile table follows it
+constexpr int kLdsMax = 160 * 1024;
 constexpr int kXcds = 8;
 
 enum Epilogue { kSwiGLU = 0, kScatter = 1 };
@@ -55,7 +61,7 @@ struct TiledArgs {
     const int32_t* offsets;
     const uint16_t* w;           // expert_weights
     uint16_t* out;               // hidden or expert_out
-    int E, K, H, I;
+    int T, E, K, H, I;
     int kdim;                    // H or I
     int ndim;                    // I (gate/up: tile covers 128 i of gate and up) or H (down)
     int ntiles_n;                // n-tiles per expert
@@ -72,161 +78,325 @@ __device__ __forceinline__ void ring_barrier() {
     __builtin_amdgcn_sched_barrier(0);
 }
 
-// Linear tile -> (expert, m-tile, n-tile); false when t is past the last tile.
-__device__ __forceinline__ bool find_tile(const TiledArgs& p, int t, int* e_out, int* mt_out, int* nt_out,
-                                          int* off_out, int* ne_out) {
-    int base = 0;
-    for (int e = 0; e < p.E; ++e) {
-        const int off = p.offsets[e];
-        const int ne = p.offsets[e + 1] - off;
-        const int mtiles = (ne + kBM - 1) / kBM;
-        const int tiles = mtiles * p.ntiles_n;
-        if (t < base + tiles) {
-            const int local = t - base;
-            *e_out = e;
-            *nt_out = local / mtiles;
-            *mt_out = local % mtiles;
-            *off_out = off;
-            *ne_out = ne;
-            return true;
-        }
-        base += tiles;
-    }
-    return false;
+// silu(g) * u with the hardware exp2 and reciprocal (each about 1 ulp): g * rcp(1 + 2^(-g log2 e)) * u.
+__device__ __forceinline__ float swiglu_fast(float g, float u) {
+#pragma clang fp contract(off)
+    const float e = __builtin_amdgcn_exp2f(g * -1.4426950408889634f);
+    return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
 }
+
+// Interleave pattern of one 16-MFMA phase: NR LDS reads and NV global->LDS copies are issued one after each of
+// its first MFMAs, so neither pipe waits for the other.
+template <int NR, int NV>
+__device__ __forceinline__ void phase_sched() {
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        if (q < NR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+        if (q < NV) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+    }
+}
+
+struct TileRef {
+    int e, mt, nt, off, ne;
+};
+
+// Copy plan of one tile: per stage and operand, wave w issues 4 instructions j, each filling 8 whole LDS rows
+// r = (4 w + j) * 8 + lane / 8 (128 B each); lane fetches global granule (lane % 8) ^ ((r >> 1) & 7). ao / bo
+// are byte offsets of those granules at k = 0 in the activation and weight buffers ar / wr.
+struct CopyPlan {
+    uint32_t ao[4], bo[4];
+    __amdgpu_buffer_rsrc_t ar, wr;
+};
 
 template <int EPI>
 __global__ __launch_bounds__(kThreads) void ffn_tiled_kernel(TiledArgs p) {
     extern __shared__ __align__(16) uint16_t lds[];
-    // XCD-contiguous remap of the dispatch order
-    const int G = static_cast<int>(gridDim.x);
-    const int per_xcd = (G + kXcds - 1) / kXcds;
-    const int b = static_cast<int>(blockIdx.x);
-    const int t = (b % kXcds) * per_xcd + b / kXcds;
-    int e, mt, nt, off, ne;
-    if (!find_tile(p, t, &e, &mt, &nt, &off, &ne)) return;
-
     const int tid = static_cast<int>(threadIdx.x);
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int lane = lane_id();
     const int row16 = lane & 15, kg = lane >> 4;
     const int wm = wave >> 2, wn = wave & 3;  // 2 x 4 waves: rows wm*128.., weight rows wn*64..
-    const int m0 = mt * kBM;
-    const size_t ebase = static_cast<size_t>(e) * 3 * static_cast<size_t>(p.I) * p.H;
 
-    // direct-to-LDS plan: per stage and operand, wave w issues 4 instructions j, each filling 8 whole LDS rows
-    // r = (4 w + j) * 8 + lane / 8 (128 B each); lane fetches global granule (lane % 8) ^ ((r >> 1) & 7)
-    uint32_t aoff[4], boff[4];
+    // Tile table in LDS after the ring: tab[e] = tiles of the experts before e (tab[E] = all tiles), offs[e] =
+    // first sorted row of expert e. Tiles are (expert, n-tile, m-tile), m fastest.
+    int* tab = reinterpret_cast<int*>(lds + kNStage * kStageHalfs);
+    int* offs = tab + (p.E + 1);
+    // Three row tables of 256 sorted-slot entries, one per tile in flight (tile k uses table k % 3): the copy rows
+    // of gate/up gather x rows by them, the down epilogue scatters by them. Wave 0 copies tile k + 1's table
+    // straight into LDS at the start of tile k; it lands before the next ring barrier.
+    int* rowtab = reinterpret_cast<int*>(lds + kNStage * kStageHalfs) + 2 * (p.E + 1);
+    if (wave == 0) {
+        int carry = 0;
+        for (int base = 0; base <= p.E; base += kWave) {
+            const int e = base + lane;
+            int o0 = 0, tiles = 0;
+            if (e <= p.E) {
+                o0 = p.offsets[e];
+                offs[e] = o0;
+            }
+            if (e < p.E) tiles = (p.offsets[e + 1] - o0 + kBM - 1) / kBM * p.ntiles_n;
+            int incl = tiles;  // inclusive scan over the wave
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int r = (wave * 4 + j) * 8 + (lane / 8);
-        const int gq = (lane % 8) ^ ((r >> 1) & 7);
-        const int m = min(m0 + r, ne - 1);
-        const uint32_t src = p.gather ? static_cast<uint32_t>(p.sorted_slot[off + m] / p.K) : static_cast<uint32_t>(off + m);
-        aoff[j] = src * static_cast<uint32_t>(p.kdim) + gq * 8;
-        if (EPI == kSwiGLU) {
-            const int quarter = r >> 6, sub = r & 63;
-            const int ic = min(nt * 128 + quarter * 32 + (sub & 31), p.I - 1);
-            boff[j] = (sub < 32 ? 0u : static_cast<uint32_t>(p.I) * p.H) + static_cast<uint32_t>(ic) * p.H + gq * 8;
-        } else {
-            const int n = min(nt * kBN + r, p.H - 1);
-            boff[j] = 2u * static_cast<uint32_t>(p.I) * p.H + static_cast<uint32_t>(n) * p.I + gq * 8;
+            for (int d = 1; d < kWave; d <<= 1) {
+                const int v = __shfl_up(incl, d, kWave);
+                if (lane >= d) incl += v;
+            }
+            if (e < p.E) tab[e + 1] = carry + incl;
+            carry += __shfl(incl, kWave - 1, kWave);
         }
+        if (lane == 0) tab[0] = 0;
     }
-    const uint16_t* abase = p.act;
-    const uint16_t* wbase = p.w + ebase;
+    __syncthreads();
+    const int total = tab[p.E];
 
-    f32x4 acc[8][4];
-    auto issue_stage = [&](int ks) {
-        const int k0 = ks * kBK;
-        uint16_t* sa = lds + (ks % kNStage) * kStageHalfs;
+    // Persistent: the grid is a multiple of 8 workgroups, at most one per CU. Workgroups are dispatched
+    // round-robin over the 8 XCDs, so workgroup b runs on XCD x = b % 8 as that XCD's li = b / 8-th workgroup.
+    // XCD x owns tiles [x * per_xcd, (x + 1) * per_xcd) (m-tiles of one weight tile are consecutive, so they
+    // share that XCD's L2), and its workgroups take them round-robin: li, li + nloc, li + 2 nloc, ...
+    const int per_xcd = (total + kXcds - 1) / kXcds;
+    const int nloc = static_cast<int>(gridDim.x) / kXcds;
+    const int x = static_cast<int>(blockIdx.x) % kXcds, li = static_cast<int>(blockIdx.x) / kXcds;
+    auto tile_at = [&](int k, TileRef& T) __attribute__((always_inline)) -> bool {
+        const int loc = li + k * nloc;
+        const int t = x * per_xcd + loc;
+        if (loc >= per_xcd || t >= total) return false;
+        int lo = 0, hi = p.E;  // tab[lo] <= t < tab[hi]
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (__builtin_amdgcn_readfirstlane(tab[mid]) <= t) lo = mid;
+            else hi = mid;
+        }
+        T.e = lo;
+        T.off = __builtin_amdgcn_readfirstlane(offs[lo]);
+        T.ne = __builtin_amdgcn_readfirstlane(offs[lo + 1]) - T.off;
+        const int mtiles = (T.ne + kBM - 1) / kBM;
+        const int local = t - __builtin_amdgcn_readfirstlane(tab[lo]);
+        T.nt = local / mtiles;
+        T.mt = local - T.nt * mtiles;
+        return true;
+    };
+    TileRef cur;
+    if (!tile_at(0, cur)) return;
+
+    // activation rows a tile copies: gate/up gathers token rows, down reads its sorted hidden rows
+    const uint32_t act_rows = p.gather ? static_cast<uint32_t>(p.T) : static_cast<uint32_t>(p.offsets[p.E]);
+    const uint32_t kbytes = static_cast<uint32_t>(p.kdim) * 2;
+    const __amdgpu_buffer_rsrc_t srsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<int32_t*>(p.sorted_slot), 0,
+                                                                          p.T * p.K * 4, 0x00020000);
+    auto load_rows = [&](const TileRef& T, int buf) __attribute__((always_inline)) {
+        if (wave == 0) {
+#pragma unroll
+            for (int jj = 0; jj < kBM / kWave; ++jj) {
+                const int r = jj * kWave + lane;
+                const int row = T.off + min(T.mt * kBM + r, T.ne - 1);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(srsrc, (__attribute__((address_space(3))) void*)(rowtab + buf * kBM + jj * kWave), 4,
+                                                         row * 4, 0, 0, 0);
+            }
+        }
+    };
+    auto make_plan = [&](const TileRef& T, int buf, CopyPlan& P) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int r = (wave * 4 + j) * 8 + (lane / 8);
+            const uint32_t gq = static_cast<uint32_t>((lane % 8) ^ ((r >> 1) & 7));
+            if (p.gather) {
+                P.ao[j] = static_cast<uint32_t>(rowtab[buf * kBM + r] / p.K) * kbytes + gq * 16;
+            } else {  // rows relative to the tile's first row
+                P.ao[j] = static_cast<uint32_t>(min(r, T.ne - 1 - T.mt * kBM)) * kbytes + gq * 16;
+            }
+            if (EPI == kSwiGLU) {
+                const int quarter = r >> 6, sub = r & 63;
+                const int ic = min(T.nt * 128 + quarter * 32 + (sub & 31), p.I - 1);
+                P.bo[j] = ((sub < 32 ? 0u : static_cast<uint32_t>(p.I)) + static_cast<uint32_t>(ic)) * static_cast<uint32_t>(p.H) * 2 + gq * 16;
+            } else {
+                const int n = min(T.nt * kBN + r, p.H - 1);
+                P.bo[j] = (2u * static_cast<uint32_t>(p.I) * p.H + static_cast<uint32_t>(n) * p.I) * 2 + gq * 16;
+            }
+        }
+        if (p.gather) {
+            P.ar = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.act), 0, static_cast<int>(act_rows * kbytes), 0x00020000);
+        } else {
+            const uint32_t row0 = static_cast<uint32_t>(T.off + T.mt * kBM);
+            P.ar = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.act + static_cast<size_t>(row0) * p.kdim), 0,
+                                                     static_cast<int>((act_rows - row0) * kbytes), 0x00020000);
+        }
+        const size_t ebase = static_cast<size_t>(T.e) * 3 * static_cast<size_t>(p.I) * p.H;
+        P.wr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.w + ebase), 0,
+                                                 static_cast<int>(3u * static_cast<uint32_t>(p.I) * p.H * 2), 0x00020000);
+    };
+
+    // copies stage kc of plan P into ring slot q % 2
+    auto copy = [&](int q, int kc, const CopyPlan& P) __attribute__((always_inline)) {
+        const int kb = kc * kBK * 2;  // byte offset of the stage along k (scalar)
+        uint16_t* sa = lds + (q % kNStage) * kStageHalfs;
         uint16_t* sb = sa + kBM * kPitch;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(abase + aoff[j] + k0),
-                                             (__attribute__((address_space(3))) void*)(sa + (wave * 4 + j) * 8 * kPitch), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(wbase + boff[j] + k0),
-                                             (__attribute__((address_space(3))) void*)(sb + (wave * 4 + j) * 8 * kPitch), 16, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(P.ar, (__attribute__((address_space(3))) void*)(sa + (wave * 4 + j) * 8 * kPitch), 16,
+                                                     static_cast<int>(P.ao[j]), kb, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(P.wr, (__attribute__((address_space(3))) void*)(sb + (wave * 4 + j) * 8 * kPitch), 16,
+                                                     static_cast<int>(P.bo[j]), kb, 0, 0);
         }
     };
-    auto mma_stage = [&](int ks, bool first) {
-        const int buf = ks % kNStage;
-        const int sw = (row16 >> 1) & 7;
-        const uint16_t* sa = lds + buf * kStageHalfs + (wm * 128 + row16) * kPitch;
-        const uint16_t* sb = lds + buf * kStageHalfs + (kBM + wn * 64 + row16) * kPitch;
+    f32x4 acc[8][4];
+    // Fragment registers: the wave's 128 rows are two halves of 4 16-row blocks (A0, A1); the 64 weight rows are
+    // 4 blocks, held for the even (Bx) and the odd (By) 32-k step of a stage.
+    f16x8 A0[4], A1[4], Bx[4], By[4];
+    const int sw = (row16 >> 1) & 7;
+    auto rdA = [&](int q, int kk, int h, f16x8 (&a)[4]) __attribute__((always_inline)) {
+        const uint16_t* sa = lds + (q % kNStage) * kStageHalfs + (wm * 128 + h * 64 + row16) * kPitch + (((kk * 4 + kg) ^ sw) * 8);
 #pragma unroll
-        for (int kk = 0; kk < kBK / 32; ++kk) {
-            const int gran = ((kk * 4 + kg) ^ sw) * 8;
-            f16x8 af[8];
+        for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const f16x8*>(sa + i * 16 * kPitch);
+    };
+    auto rdB = [&](int q, int kk, f16x8 (&bb)[4]) __attribute__((always_inline)) {
+        const uint16_t* sb = lds + (q % kNStage) * kStageHalfs + (kBM + wn * 64 + row16) * kPitch + (((kk * 4 + kg) ^ sw) * 8);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) af[i] = *reinterpret_cast<const f16x8*>(sa + i * 16 * kPitch + gran);
+        for (int j = 0; j < 4; ++j) bb[j] = *reinterpret_cast<const f16x8*>(sb + j * 16 * kPitch);
+    };
+    // D[weight row][activation row]: each lane ends with 4 consecutive output columns of one row
+    auto mma = [&](int h, const f16x8 (&a)[4], const f16x8 (&bb)[4], bool zero) __attribute__((always_inline)) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const f16x8 bf = *reinterpret_cast<const f16x8*>(sb + j * 16 * kPitch + gran);
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int i = 0; i < 8; ++i)
-                    acc[i][j] = mfma16x16x32(af[i], bf, first && kk == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[i][j]);
-            }
-        }
+            for (int j = 0; j < 4; ++j)
+                acc[h * 4 + i][j] = mfma16x16x32(bb[j], a[i], zero ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[h * 4 + i][j]);
     };
 
-    // two LDS stages: stage s + 1 is copied into the other buffer while stage s is multiplied
-    const int nstages = p.kdim / kBK;
-    issue_stage(0);
+    // The ring of two LDS slots runs over this workgroup's tiles back to back: ring index q counts stages over
+    // all its tiles, and the copies of a tile's first two stages are issued during the previous tile's last two.
+    // Stage q multiplies its two 32-k steps in four phases of 16 MFMAs: (kk0, A0), (kk0, A1), (kk1, A0),
+    // (kk1, A1). Each phase reads the fragments that the next phase or the one after needs. Between the third and
+    // the fourth phase the wave has read all of stage q from LDS: one barrier then publishes stage q + 1 (every
+    // wave's copies have landed) and frees slot q % 2 for the copies of ring stage q + 2 (stage kc of plan P).
+    // After the last tile those copies repeat its last stage into the free slot and the fourth phase reads
+    // fragments nobody uses.
+    auto stage = [&](int q, bool first, int kc, const CopyPlan& P) __attribute__((always_inline)) {
+        __builtin_amdgcn_sched_barrier(0);
+        mma(0, A0, Bx, first);
+        rdA(q, 0, 1, A1);
+        rdB(q, 1, By);
+        phase_sched<8, 0>();
+        __builtin_amdgcn_sched_barrier(0);
+        mma(1, A1, Bx, first);
+        rdA(q, 1, 0, A0);
+        phase_sched<4, 0>();
+        __builtin_amdgcn_sched_barrier(0);
+        mma(0, A0, By, false);
+        rdA(q, 1, 1, A1);
+        phase_sched<4, 0>();
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // this wave's copies of ring stage q + 1
+        __builtin_amdgcn_s_waitcnt(0xc07f);        // lgkmcnt(0): this wave's reads of ring stage q are done
+        ring_barrier();
+        copy(q + 2, kc, P);
+        mma(1, A1, By, false);
+        rdB(q + 1, 0, Bx);
+        rdA(q + 1, 0, 0, A0);
+        phase_sched<8, 8>();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    const int nst = p.kdim / kBK;  // >= 2
+    CopyPlan plan;
+    load_rows(cur, 0);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    __syncthreads();
+    make_plan(cur, 0, plan);
+    copy(0, 0, plan);
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // this wave's copies of stage 0 are in LDS
     ring_barrier();                            // and every wave's
-    if (nstages > 1) issue_stage(1);
-    mma_stage(0, true);  // the accumulators start from an inline zero, so they are never VGPR-initialised
-    if (nstages > 1) {
-        __builtin_amdgcn_sched_barrier(0);  // keep the copy wait after every MFMA of the stage
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-        ring_barrier();
-        for (int s = 1; s + 1 < nstages; ++s) {
-            issue_stage(s + 1);  // into the buffer stage s - 1 used: the barrier above ended its reads
-            mma_stage(s, false);
-            __builtin_amdgcn_sched_barrier(0);
+    copy(1, 1, plan);
+    rdB(0, 0, Bx);
+    rdA(0, 0, 0, A0);
+    int q0 = 0;  // ring index of the current tile's first stage
+    for (int k = 0;; ++k) {
+        TileRef nxt;
+        const bool has_next = tile_at(k + 1, nxt);
+        // table k + 1 % 3 was last read two tiles ago; the barriers of tile k - 1 separate those reads from this copy
+        if (has_next) load_rows(nxt, (k + 1) % 3);
+        // the last two stages copy the next tile's first two (or, after the last tile, repeat this tile's last)
+        const int kc0 = has_next ? 0 : nst - 1, kc1 = has_next ? 1 : nst - 1;
+        if (nst > 2) {
+            stage(q0, true, 2, plan);
+            for (int s = 1; s + 2 < nst; ++s) stage(q0 + s, false, s + 2, plan);
+            if (has_next) make_plan(nxt, (k + 1) % 3, plan);
+            stage(q0 + nst - 2, false, kc0, plan);
+            stage(q0 + nst - 1, false, kc1, plan);
+        } else {  // the next tile's plan is needed before the first barrier: wait for its row table here
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-            ring_barrier();
+            __syncthreads();
+            if (has_next) make_plan(nxt, (k + 1) % 3, plan);
+            stage(q0, true, kc0, plan);
+            stage(q0 + 1, false, kc1, plan);
         }
-        mma_stage(nstages - 1, false);
-    }
 
-    // ---- epilogue: acc[i][j] lane holds D[m = 4*kg + r][n = row16] of sub-tile (i, j) ----
+        // ---- epilogue: acc[i][j] lane holds D[weight row 4*kg + r of block j][activation row row16 of block i],
+        // i.e. 4 consecutive output columns of one row: one 8-byte store per (i, j) ----
+        const int m = cur.mt * kBM + wm * 128 + row16;
+        if (EPI == kSwiGLU) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int m = m0 + wm * 128 + i * 16 + kg * 4 + r;
-            if (m >= ne) continue;
-            if (EPI == kSwiGLU) {
-                uint16_t* dst = p.out + static_cast<size_t>(off + m) * p.I;
+            for (int i = 0; i < 8; ++i) {
+                if (m + i * 16 >= cur.ne) continue;
+                uint16_t* dst = p.out + static_cast<size_t>(cur.off + m + i * 16) * p.I;
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
-                    const int col = nt * 128 + wn * 32 + j * 16 + row16;
-                    if (col < p.I) dst[col] = f32_to_f16_bits(swiglu_f32(acc[i][j][r], acc[i][j + 2][r]));
+                    const int col = cur.nt * 128 + wn * 32 + j * 16 + kg * 4;
+                    if (col >= p.I) continue;
+                    const uint32_t lo = f32_to_f16_bits(swiglu_fast(acc[i][j][0], acc[i][j + 2][0])) |
+                                        (static_cast<uint32_t>(f32_to_f16_bits(swiglu_fast(acc[i][j][1], acc[i][j + 2][1]))) << 16);
+                    const uint32_t hi = f32_to_f16_bits(swiglu_fast(acc[i][j][2], acc[i][j + 2][2])) |
+                                        (static_cast<uint32_t>(f32_to_f16_bits(swiglu_fast(acc[i][j][3], acc[i][j + 2][3]))) << 16);
+                    *reinterpret_cast<uint2*>(dst + col) = make_uint2(lo, hi);
                 }
-            } else {
-                uint16_t* dst = p.out + static_cast<size_t>(p.sorted_slot[off + m]) * p.H;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                if (m + i * 16 >= cur.ne) continue;
+                uint16_t* dst = p.out + static_cast<size_t>(rowtab[(k % 3) * kBM + wm * 128 + i * 16 + row16]) * p.H;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const int col = nt * kBN + wn * 64 + j * 16 + row16;
-                    if (col < p.H) dst[col] = f32_to_f16_bits(acc[i][j][r]);
+                    const int col = cur.nt * kBN + wn * 64 + j * 16 + kg * 4;
+                    if (col >= p.H) continue;
+                    const uint32_t lo = f32_to_f16_bits(acc[i][j][0]) | (static_cast<uint32_t>(f32_to_f16_bits(acc[i][j][1])) << 16);
+                    const uint32_t hi = f32_to_f16_bits(acc[i][j][2]) | (static_cast<uint32_t>(f32_to_f16_bits(acc[i][j][3])) << 16);
+                    *reinterpret_cast<uint2*>(dst + col) = make_uint2(lo, hi);
                 }
             }
         }
+        if (!has_next) break;
+        cur = nxt;
+        q0 += nst;
+    }
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // the surplus copies have landed before the workgroup ends
 }
 
 template <int EPI>
 hipError_t launch_tiled(const TiledArgs& p, int grid, hipStream_t stream) {
-    const hipError_t attr = ensure_lds_limit(reinterpret_cast<const void*>(&ffn_tiled_kernel<EPI>), kLdsBytes);
+    const void* fn = reinterpret_cast<const void*>(&ffn_tiled_kernel<EPI>);
+    const hipError_t attr = ensure_lds_limit(fn, kLdsMax);
     if (attr != hipSuccess) return attr;
-    ffn_tiled_kernel<EPI><<<grid, kThreads, kLdsBytes, stream>>>(p);
+    const int lds = kLdsBytes + 8 * (p.E + 1) + 3 * kBM * 4;
+    // persistent: at most the workgroups the device holds at once, a multiple of the XCD count
+    const int resident = resident_workgroups(fn, kThreads, lds);
+    if (EPI == kSwiGLU && resident > 0 && resident < grid) grid = resident;
+    grid = grid / kXcds * kXcds;
+    if (grid < kXcds) grid = kXcds;
+    ffn_tiled_kernel<EPI><<<grid, kThreads, lds, stream>>>(p);
     return hipGetLastError();
 }
 
 }  // namespace
 
-bool tiled_supported(int H, int I) { return H % kBK == 0 && I % kBK == 0; }
+// Both k extents need at least two stages (the ring runs two ahead); the buffer offsets are 32-bit; the tile
+// table must fit in the LDS left over by the ring.
+bool tiled_supported(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
+    if (H % kBK != 0 || I % kBK != 0 || H < 2 * kBK || I < 2 * kBK) return false;
+    const int64_t lim = int64_t(1) << 31;
+    if (T * H * 2 >= lim || T * K * I * 2 >= lim || 3 * I * H * 2 >= lim || T * K * 4 >= lim) return false;
+    return kLdsBytes + 8 * (E + 1) + 3 * kBM * 4 <= kLdsMax;
+}
 int tiled_block_threads() { return kThreads; }
 int tiled_rows_per_tile() { return kBM; }
 // Upper bound on the tile count (sum over experts of ceil(rows_e / kBM) <= ceil(T*K / kBM) + E), rounded up to
@@ -245,6 +415,7 @@ hipError_t launch_ffn_tiled(const uint16_t* x, const uint16_t* expert_weights, u
     p.sorted_slot = ws.sorted_slot;
     p.offsets = ws.offsets;
     p.w = expert_weights;
+    p.T = T;
     p.E = E;
     p.K = K;
     p.H = H;

@@ -73,7 +73,7 @@ hipError_t launch_ffn_stream(const uint16_t* x, const int32_t* expert_ids, const
                              uint16_t* expert_out, const FfnWorkspace& ws, int T, int H, int E, int K, int I,
                              hipStream_t stream, const uint16_t* weights = nullptr, uint16_t* y = nullptr);
 // LDS-tiled schedule (moe_ffn_tiled.hip)
-bool tiled_supported(int H, int I);
+bool tiled_supported(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I);
 int tiled_block_threads();
 int tiled_rows_per_tile();
 int tiled_gateup_grid(int T, int E, int K, int I);

@@ -429,10 +429,10 @@ def ffn_schedule(T, H, E, K, I) -> int:
 @pytest.mark.parametrize("T,H,E,K,I", [
     (300, 128, 4, 2, 128),    # partial m-tiles (~150 rows per expert)
     (257, 320, 3, 2, 192),    # partial n-tiles in both GEMMs (I = 192 -> 2 x 128, H = 320 -> 2 x 256)
-    (600, 64, 8, 3, 64),      # K = 3, single k-stage
-    (700, 192, 2, 1, 1408),   # >256 rows per expert (several m-tiles), DeepSeek's I
-    (8200, 64, 256, 2, 64),   # E = 256: the permute re-reads expert_ids instead of its LDS byte copy
-    (900, 64, 8, 2, 64),      # ids outside [0, E) through the permute's LDS byte copy (sentinel 255)
+    (600, 128, 8, 3, 128),    # K = 3, two k-stages in both GEMMs (the shortest ring)
+    (700, 192, 2, 1, 1408),   # >256 rows per expert (several m-tiles), DeepSeek's I, three k-stages
+    (8200, 128, 256, 2, 128), # E = 256: the permute re-reads expert_ids instead of its LDS byte copy
+    (900, 128, 8, 2, 128),    # ids outside [0, E) through the permute's LDS byte copy (sentinel 255)
 ])
 def test_ffn_tiled_schedule_full_oracle(ops, T, H, E, K, I):
     assert ffn_schedule(T, H, E, K, I) == 1
@@ -453,6 +453,28 @@ def test_ffn_tiled_schedule_full_oracle(ops, T, H, E, K, I):
     eo_o = oracle.expert_ffn(f32(x), np.where(valid, ids, 0), f32(ew), I)
     m = oracle.compare(eo[valid], eo_o[valid])
     log(f"[tiled T{T} H{H} E{E} K{K} I{I}] expert_out vs oracle: {m}")
+    within(m, max_abs=1e-2, mean_abs=1e-3, cos=0.9999)
+
+
+def test_ffn_tiled_several_tiles_per_workgroup(ops):
+    """512 gate/up tiles on a grid of at most one workgroup per CU: each workgroup runs several tiles with the
+    copy ring running on from one tile into the next (other experts, other n-tiles). Checked against the oracle
+    on 256 sampled tokens, which touch every (expert, m-tile) row block."""
+    T, H, E, K, I = 4096, 256, 4, 2, 2048
+    assert ffn_schedule(T, H, E, K, I) == 1
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((T, H)).astype(np.float16)
+    ew = np.concatenate([rng.standard_normal((E, 2 * I, H)) / math.sqrt(H),
+                         rng.standard_normal((E, I, H)) / math.sqrt(I)], axis=1).astype(np.float16)
+    ids = np.stack([rng.permutation(E)[:K] for _ in range(T)]).astype(np.int32)
+    w = np.full((T, K), 1.0 / K, np.float16)
+    eo_d, ws = run_ffn(ops, dev(x), dev(ids), dev(w), dev(ew), I)
+    check_permute(host(ws), ids, E)
+    eo = f32(host(eo_d))
+    tok = np.sort(rng.choice(T, 256, replace=False))
+    eo_o = oracle.expert_ffn(f32(x[tok]), ids[tok], f32(ew), I)
+    m = oracle.compare(eo[tok], eo_o)
+    log(f"[tiled multi-tile T{T} H{H} E{E} K{K} I{I}] expert_out vs oracle on 256 tokens: {m}")
     within(m, max_abs=1e-2, mean_abs=1e-3, cos=0.9999)
 
 
