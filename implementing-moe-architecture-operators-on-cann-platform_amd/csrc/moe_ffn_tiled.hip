@@ -52,6 +52,10 @@ constexpr int kNStage = 2;
 constexpr int kLdsBytes = kNStage * kStageHalfs * 2;  // the ring; the tile table follows it
 constexpr int kLdsMax = 160 * 1024;
 constexpr int kXcds = 8;
+// Partial tiles of the split leftover round: one fp32 kBM x kBN tile per workgroup of a persistent launch.
+constexpr int kMaxParts = 256;
+constexpr int kFixThreads = 256;
+constexpr int kFixRows = 16;  // tile rows per fix-up workgroup
 
 enum Epilogue { kSwiGLU = 0, kScatter = 1 };
 
@@ -66,7 +70,27 @@ struct TiledArgs {
     int ndim;                    // I (gate/up: tile covers 128 i of gate and up) or H (down)
     int ntiles_n;                // n-tiles per expert
     int gather;                  // gate/up: activation row r -> x[sorted_slot[r] / K]
+    int split;                   // split the leftover tiles of each XCD over k (persistent grid <= kMaxParts)
+    float* partial;              // [kMaxParts, kBM, kBN] fp32 partial tiles of the split leftover round
 };
+
+// Work of one XCD: its tiles [base, base + n) are dealt to its nloc workgroups in R full rounds; the L tiles
+// left over are each split over k into S pieces of at least two stages, one piece per workgroup, so the last
+// round keeps every workgroup busy instead of L of them. S = 1 runs the leftover tiles whole.
+struct XcdSched {
+    int base, n, R, L, S;
+};
+__device__ __forceinline__ XcdSched xcd_sched(int x, int total, int nloc, int nst, int split) {
+    XcdSched s;
+    const int per_xcd = (total + kXcds - 1) / kXcds;
+    s.base = x * per_xcd;
+    s.n = max(0, min(per_xcd, total - s.base));
+    s.R = s.n / nloc;
+    s.L = s.n - s.R * nloc;
+    s.S = 1;
+    if (split && s.L > 0) s.S = max(1, min(nloc / s.L, nst / 2));
+    return s;
+}
 
 // Barrier of the copy ring. The only LDS writes of the main loop are this wave's direct-to-LDS copies, which the
 // caller's explicit vmcnt wait covers, and every fragment read of the stage has fed an MFMA before the wave gets
@@ -97,8 +121,11 @@ __device__ __forceinline__ void phase_sched() {
     }
 }
 
+// One work item: tile (e, mt, nt), k-stages [k0, k0 + nk), and the partial slot it writes (-1: the whole k
+// range, written through the epilogue).
 struct TileRef {
     int e, mt, nt, off, ne;
+    int k0, nk, part;
 };
 
 // Copy plan of one tile: per stage and operand, wave w issues 4 instructions j, each filling 8 whole LDS rows
@@ -109,7 +136,9 @@ struct CopyPlan {
     __amdgpu_buffer_rsrc_t ar, wr;
 };
 
-template <int EPI>
+// SPLIT: the leftover round may be split over k (p.split); a separate instantiation, so the kernel without it
+// keeps its register allocation at tile changes.
+template <int EPI, bool SPLIT>
 __global__ __launch_bounds__(kThreads) void ffn_tiled_kernel(TiledArgs p) {
     extern __shared__ __align__(16) uint16_t lds[];
     const int tid = static_cast<int>(threadIdx.x);
@@ -153,14 +182,42 @@ __global__ __launch_bounds__(kThreads) void ffn_tiled_kernel(TiledArgs p) {
     // Persistent: the grid is a multiple of 8 workgroups, at most one per CU. Workgroups are dispatched
     // round-robin over the 8 XCDs, so workgroup b runs on XCD x = b % 8 as that XCD's li = b / 8-th workgroup.
     // XCD x owns tiles [x * per_xcd, (x + 1) * per_xcd) (m-tiles of one weight tile are consecutive, so they
-    // share that XCD's L2), and its workgroups take them round-robin: li, li + nloc, li + 2 nloc, ...
-    const int per_xcd = (total + kXcds - 1) / kXcds;
+    // share that XCD's L2), and its workgroups take them round-robin: li, li + nloc, li + 2 nloc, ...; with
+    // p.split the tiles left over after the full rounds are split over k (xcd_sched).
+    const int nst = p.kdim / kBK;  // >= 2
     const int nloc = static_cast<int>(gridDim.x) / kXcds;
     const int x = static_cast<int>(blockIdx.x) % kXcds, li = static_cast<int>(blockIdx.x) / kXcds;
+    const int per_xcd = (total + kXcds - 1) / kXcds;
+    XcdSched xs{};
+    if (SPLIT) xs = xcd_sched(x, total, nloc, nst, p.split);
     auto tile_at = [&](int k, TileRef& T) __attribute__((always_inline)) -> bool {
-        const int loc = li + k * nloc;
-        const int t = x * per_xcd + loc;
-        if (loc >= per_xcd || t >= total) return false;
+        int t;
+        T.k0 = 0;
+        T.nk = nst;
+        T.part = -1;
+        if (!SPLIT) {
+            const int loc = li + k * nloc;
+            t = x * per_xcd + loc;
+            if (loc >= per_xcd || t >= total) return false;
+        } else {
+            int loc;
+            if (k < xs.R) {
+                loc = li + k * nloc;
+            } else if (k == xs.R && xs.S == 1) {
+                if (li >= xs.L) return false;
+                loc = xs.R * nloc + li;
+            } else if (k == xs.R) {  // piece pc of leftover tile j
+                const int j = li / xs.S, pc = li - j * xs.S;
+                if (j >= xs.L) return false;
+                loc = xs.R * nloc + j;
+                T.k0 = pc * nst / xs.S;
+                T.nk = (pc + 1) * nst / xs.S - T.k0;
+                T.part = static_cast<int>(blockIdx.x);
+            } else {
+                return false;
+            }
+            t = xs.base + loc;
+        }
         int lo = 0, hi = p.E;  // tab[lo] <= t < tab[hi]
         while (hi - lo > 1) {
             const int mid = (lo + hi) >> 1;
@@ -297,32 +354,33 @@ __global__ __launch_bounds__(kThreads) void ffn_tiled_kernel(TiledArgs p) {
         __builtin_amdgcn_sched_barrier(0);
     };
 
-    const int nst = p.kdim / kBK;  // >= 2
     CopyPlan plan;
     load_rows(cur, 0);
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     __syncthreads();
     make_plan(cur, 0, plan);
-    copy(0, 0, plan);
+    copy(0, SPLIT ? cur.k0 : 0, plan);
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // this wave's copies of stage 0 are in LDS
     ring_barrier();                            // and every wave's
-    copy(1, 1, plan);
+    copy(1, SPLIT ? cur.k0 + 1 : 1, plan);
     rdB(0, 0, Bx);
     rdA(0, 0, 0, A0);
-    int q0 = 0;  // ring index of the current tile's first stage
+    int q0 = 0;  // ring index of the current item's first stage
     for (int k = 0;; ++k) {
         TileRef nxt;
         const bool has_next = tile_at(k + 1, nxt);
         // table k + 1 % 3 was last read two tiles ago; the barriers of tile k - 1 separate those reads from this copy
         if (has_next) load_rows(nxt, (k + 1) % 3);
-        // the last two stages copy the next tile's first two (or, after the last tile, repeat this tile's last)
-        const int kc0 = has_next ? 0 : nst - 1, kc1 = has_next ? 1 : nst - 1;
-        if (nst > 2) {
-            stage(q0, true, 2, plan);
-            for (int s = 1; s + 2 < nst; ++s) stage(q0 + s, false, s + 2, plan);
+        // the last two stages copy the next item's first two (or, after the last item, repeat this one's last)
+        const int k0 = SPLIT ? cur.k0 : 0, nk = SPLIT ? cur.nk : nst;  // nk >= 2
+        const int nk0 = SPLIT ? nxt.k0 : 0;
+        const int kc0 = has_next ? nk0 : k0 + nk - 1, kc1 = has_next ? nk0 + 1 : k0 + nk - 1;
+        if (nk > 2) {
+            stage(q0, true, k0 + 2, plan);
+            for (int s = 1; s + 2 < nk; ++s) stage(q0 + s, false, k0 + s + 2, plan);
             if (has_next) make_plan(nxt, (k + 1) % 3, plan);
-            stage(q0 + nst - 2, false, kc0, plan);
-            stage(q0 + nst - 1, false, kc1, plan);
+            stage(q0 + nk - 2, false, kc0, plan);
+            stage(q0 + nk - 1, false, kc1, plan);
         } else {  // the next tile's plan is needed before the first barrier: wait for its row table here
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
             __syncthreads();
@@ -334,7 +392,14 @@ __global__ __launch_bounds__(kThreads) void ffn_tiled_kernel(TiledArgs p) {
         // ---- epilogue: acc[i][j] lane holds D[weight row 4*kg + r of block j][activation row row16 of block i],
         // i.e. 4 consecutive output columns of one row: one 8-byte store per (i, j) ----
         const int m = cur.mt * kBM + wm * 128 + row16;
-        if (EPI == kSwiGLU) {
+        if (SPLIT && cur.part >= 0) {
+            // a piece of a split tile: the raw fp32 sums of its k-range, [activation row][weight row] of the tile
+            float* dst = p.partial + static_cast<size_t>(cur.part) * (kBM * kBN) + (wm * 128 + row16) * kBN + wn * 64 + kg * 4;
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) *reinterpret_cast<f32x4*>(dst + i * 16 * kBN + j * 16) = acc[i][j];
+        } else if (EPI == kSwiGLU) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 if (m + i * 16 >= cur.ne) continue;
@@ -367,23 +432,143 @@ __global__ __launch_bounds__(kThreads) void ffn_tiled_kernel(TiledArgs p) {
         }
         if (!has_next) break;
         cur = nxt;
-        q0 += nst;
+        q0 += nk;
     }
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // the surplus copies have landed before the workgroup ends
 }
 
+// Adds the pieces of each split leftover tile in piece order (fixed, so the result does not depend on timing) and
+// applies the tile's epilogue. Workgroup (g, rb) takes rows [rb * kFixRows, +kFixRows) of leftover tile
+// j = g / 8 of XCD x = g % 8; piece pc of that tile is in the partial slot of workgroup (j * S + pc) * 8 + x of the
+// tiled launch, whose grid had nloc workgroups per XCD. The tile is found as the tiled kernel finds it, from
+// offsets (each wave scans the experts 64 at a time).
 template <int EPI>
-hipError_t launch_tiled(const TiledArgs& p, int grid, hipStream_t stream) {
-    const void* fn = reinterpret_cast<const void*>(&ffn_tiled_kernel<EPI>);
+__global__ __launch_bounds__(kFixThreads) void ffn_tiled_fixup_kernel(TiledArgs p, int nloc) {
+    constexpr int nrb = kBM / kFixRows;
+    const int rb = static_cast<int>(blockIdx.x) % nrb, g = static_cast<int>(blockIdx.x) / nrb;
+    const int x = g % kXcds, j = g / kXcds;
+    const int lane = lane_id();
+    auto tiles_of = [&](int e) {
+        return e < p.E ? (p.offsets[e + 1] - p.offsets[e] + kBM - 1) / kBM * p.ntiles_n : 0;
+    };
+    int total = 0;
+    for (int base = 0; base < p.E; base += kWave) {
+        int v = tiles_of(base + lane);
+#pragma unroll
+        for (int d = 1; d < kWave; d <<= 1) v += __shfl_xor(v, d, kWave);
+        total += v;
+    }
+    const XcdSched xs = xcd_sched(x, total, nloc, p.kdim / kBK, 1);
+    if (xs.S < 2 || j >= xs.L) return;
+    const int t = xs.base + xs.R * nloc + j;
+    // expert e with prefix(e) <= t < prefix(e) + tiles(e), prefix(e) = tiles of the experts before e
+    int e = -1, before = 0, carry = 0;
+    for (int base = 0; base < p.E && e < 0; base += kWave) {
+        const int te = tiles_of(base + lane);
+        int incl = te;
+#pragma unroll
+        for (int d = 1; d < kWave; d <<= 1) {
+            const int v = __shfl_up(incl, d, kWave);
+            if (lane >= d) incl += v;
+        }
+        const uint64_t hit = __ballot(te > 0 && carry + incl - te <= t && t < carry + incl);
+        if (hit) {
+            const int l = __builtin_ctzll(hit);
+            e = base + l;
+            before = carry + __shfl(incl - te, l, kWave);
+        }
+        carry += __shfl(incl, kWave - 1, kWave);
+    }
+    const int mt_count = (p.offsets[e + 1] - p.offsets[e] + kBM - 1) / kBM;
+    const int local = t - before, nt = local / mt_count, mt = local - nt * mt_count;
+    const int off = p.offsets[e], rows = min(kBM, p.offsets[e + 1] - off - mt * kBM);
+    const float* part0 = p.partial + static_cast<size_t>(j * xs.S * kXcds + x) * (kBM * kBN);
+    const size_t pstride = static_cast<size_t>(kXcds) * (kBM * kBN);  // next piece: li + 1
+    const int tid = static_cast<int>(threadIdx.x);
+    if (EPI == kScatter) {
+        // 64 threads per row, 4 consecutive output columns each; 4 rows per thread, loaded together
+        constexpr int kRows = kFixRows / (kFixThreads / 64);
+        const int c = (tid % 64) * 4, r0 = rb * kFixRows + tid / 64;
+        const float* src = part0 + r0 * kBN + c;
+        f32x4 v[kRows];
+#pragma unroll
+        for (int u = 0; u < kRows; ++u) v[u] = *reinterpret_cast<const f32x4*>(src + u * (kFixThreads / 64) * kBN);
+#pragma unroll 2
+        for (int pc = 1; pc < xs.S; ++pc)
+#pragma unroll
+            for (int u = 0; u < kRows; ++u)
+                v[u] += *reinterpret_cast<const f32x4*>(src + pc * pstride + u * (kFixThreads / 64) * kBN);
+        const int col = nt * kBN + c;
+#pragma unroll
+        for (int u = 0; u < kRows; ++u) {
+            const int r = r0 + u * (kFixThreads / 64);
+            if (r >= rows || col >= p.H) continue;
+            const uint32_t lo = f32_to_f16_bits(v[u][0]) | (static_cast<uint32_t>(f32_to_f16_bits(v[u][1])) << 16);
+            const uint32_t hi = f32_to_f16_bits(v[u][2]) | (static_cast<uint32_t>(f32_to_f16_bits(v[u][3])) << 16);
+            const int slot = p.sorted_slot[off + mt * kBM + r];
+            *reinterpret_cast<uint2*>(p.out + static_cast<size_t>(slot) * p.H + col) = make_uint2(lo, hi);
+        }
+    } else {
+        // 32 threads per row, 4 consecutive hidden columns each; hidden column hc of the tile is weight-row column
+        // (hc / 32) * 64 + hc % 32 (gate) and 32 past it (up); 2 rows per thread, loaded together
+        constexpr int kRows = kFixRows / (kFixThreads / 32);
+        const int hc = (tid % 32) * 4, r0 = rb * kFixRows + tid / 32;
+        const float* src = part0 + r0 * kBN + (hc / 32) * 64 + hc % 32;
+        f32x4 gv[kRows], uv[kRows];
+#pragma unroll
+        for (int u = 0; u < kRows; ++u) {
+            gv[u] = *reinterpret_cast<const f32x4*>(src + u * (kFixThreads / 32) * kBN);
+            uv[u] = *reinterpret_cast<const f32x4*>(src + u * (kFixThreads / 32) * kBN + 32);
+        }
+#pragma unroll 2
+        for (int pc = 1; pc < xs.S; ++pc)
+#pragma unroll
+            for (int u = 0; u < kRows; ++u) {
+                gv[u] += *reinterpret_cast<const f32x4*>(src + pc * pstride + u * (kFixThreads / 32) * kBN);
+                uv[u] += *reinterpret_cast<const f32x4*>(src + pc * pstride + u * (kFixThreads / 32) * kBN + 32);
+            }
+        const int col = nt * 128 + hc;
+#pragma unroll
+        for (int u = 0; u < kRows; ++u) {
+            const int r = r0 + u * (kFixThreads / 32);
+            if (r >= rows || col >= p.I) continue;
+            const uint32_t lo = f32_to_f16_bits(swiglu_fast(gv[u][0], uv[u][0])) |
+                                (static_cast<uint32_t>(f32_to_f16_bits(swiglu_fast(gv[u][1], uv[u][1]))) << 16);
+            const uint32_t hi = f32_to_f16_bits(swiglu_fast(gv[u][2], uv[u][2])) |
+                                (static_cast<uint32_t>(f32_to_f16_bits(swiglu_fast(gv[u][3], uv[u][3]))) << 16);
+            *reinterpret_cast<uint2*>(p.out + static_cast<size_t>(off + mt * kBM + r) * p.I + col) = make_uint2(lo, hi);
+        }
+    }
+}
+
+// use_split: persistent grid with the leftover tiles split over k, then the fix-up kernel
+template <int EPI>
+hipError_t launch_tiled(TiledArgs p, int grid, bool persistent, bool use_split, const char* name,
+                        const char* fix_name, hipStream_t stream) {
+    const void* fn = use_split ? reinterpret_cast<const void*>(&ffn_tiled_kernel<EPI, true>)
+                               : reinterpret_cast<const void*>(&ffn_tiled_kernel<EPI, false>);
     const hipError_t attr = ensure_lds_limit(fn, kLdsMax);
     if (attr != hipSuccess) return attr;
     const int lds = kLdsBytes + 8 * (p.E + 1) + 3 * kBM * 4;
     // persistent: at most the workgroups the device holds at once, a multiple of the XCD count
     const int resident = resident_workgroups(fn, kThreads, lds);
-    if (EPI == kSwiGLU && resident > 0 && resident < grid) grid = resident;
+    if (persistent && resident > 0 && resident < grid) grid = resident;
     grid = grid / kXcds * kXcds;
     if (grid < kXcds) grid = kXcds;
-    ffn_tiled_kernel<EPI><<<grid, kThreads, lds, stream>>>(p);
+    // a split needs the persistent grid (the leftover round is sized by the workgroups per XCD) and one partial
+    // slot per workgroup
+    p.split = (use_split && persistent && resident > 0 && grid <= resident && grid <= kMaxParts) ? 1 : 0;
+    {
+        TraceScope trace(name, stream);
+        if (use_split) ffn_tiled_kernel<EPI, true><<<grid, kThreads, lds, stream>>>(p);
+        else ffn_tiled_kernel<EPI, false><<<grid, kThreads, lds, stream>>>(p);
+    }
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess || !p.split) return err;
+    {
+        TraceScope trace(fix_name, stream);
+        ffn_tiled_fixup_kernel<EPI><<<grid * (kBM / kFixRows), kFixThreads, 0, stream>>>(p, grid / kXcds);
+    }
     return hipGetLastError();
 }
 
@@ -398,6 +583,7 @@ bool tiled_supported(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
     return kLdsBytes + 8 * (E + 1) + 3 * kBM * 4 <= kLdsMax;
 }
 int tiled_block_threads() { return kThreads; }
+size_t tiled_partial_bytes() { return static_cast<size_t>(kMaxParts) * kBM * kBN * sizeof(float); }
 int tiled_rows_per_tile() { return kBM; }
 // Upper bound on the tile count (sum over experts of ceil(rows_e / kBM) <= ceil(T*K / kBM) + E), rounded up to
 // a multiple of the XCD count so that the XCD-contiguous remap in the kernel is a bijection on [0, grid).
@@ -426,11 +612,9 @@ hipError_t launch_ffn_tiled(const uint16_t* x, const uint16_t* expert_weights, u
     p.ndim = I;
     p.ntiles_n = (I + 127) / 128;
     p.gather = 1;
-    hipError_t err;
-    {
-        TraceScope trace("moe_ffn_gateup_swiglu", stream);
-        err = launch_tiled<kSwiGLU>(p, tiled_gateup_grid(T, E, K, I), stream);
-    }
+    p.partial = ws.partial;
+    const hipError_t err = launch_tiled<kSwiGLU>(p, tiled_gateup_grid(T, E, K, I), true, false,
+                                                 "moe_ffn_gateup_swiglu", "moe_ffn_gateup_fixup", stream);
     if (err != hipSuccess) return err;
     p.act = ws.hidden;
     p.out = expert_out;
@@ -438,11 +622,8 @@ hipError_t launch_ffn_tiled(const uint16_t* x, const uint16_t* expert_weights, u
     p.ndim = H;
     p.ntiles_n = (H + kBN - 1) / kBN;
     p.gather = 0;
-    {
-        TraceScope trace("moe_ffn_down", stream);
-        err = launch_tiled<kScatter>(p, tiled_down_grid(T, E, K, H), stream);
-    }
-    return err;
+    return launch_tiled<kScatter>(p, tiled_down_grid(T, E, K, H), true, true, "moe_ffn_down", "moe_ffn_down_fixup",
+                                  stream);
 }
 
 }  // namespace moe

@@ -42,7 +42,8 @@ struct FfnWorkspace {
     int32_t* offsets;      // [E + 1] first sorted row of each expert; offsets[E] = number of valid slots
     int32_t* sorted_slot;  // [T*K]   slot index t*K + k of each sorted row, experts ascending, slots ascending
     uint16_t* hidden;      // [T*K, I] fp16 SwiGLU intermediate, rows in sorted order
-    float* partial;        // [nsplit, T*K, H] fp32 split-K partial sums of the down projection (may be empty)
+    float* partial;        // fp32 split-K partial sums: [nsplit, T*K, H] of the streaming down projection, or the
+                           // tiled schedule's partial tiles of its split leftover round
     int32_t* slot_row;     // [T*K]   sorted row of each slot with a valid id (weight-streaming schedule only)
 };
 size_t ffn_workspace_bytes(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I);
@@ -75,6 +76,8 @@ hipError_t launch_ffn_stream(const uint16_t* x, const int32_t* expert_ids, const
 // LDS-tiled schedule (moe_ffn_tiled.hip)
 bool tiled_supported(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I);
 int tiled_block_threads();
+// fp32 partial tiles of the split leftover round (workspace region after hidden)
+size_t tiled_partial_bytes();
 int tiled_rows_per_tile();
 int tiled_gateup_grid(int T, int E, int K, int I);
 int tiled_down_grid(int T, int E, int K, int H);

@@ -478,6 +478,36 @@ def test_ffn_tiled_several_tiles_per_workgroup(ops):
     within(m, max_abs=1e-2, mean_abs=1e-3, cos=0.9999)
 
 
+def test_ffn_tiled_split_leftover_round(ops):
+    """~560 down tiles on the persistent grid: two full rounds per workgroup, then each XCD's leftover tiles split
+    over k into pieces (fp32 partial tiles) that the fix-up kernel adds in piece order. Checked against the oracle
+    on 192 sampled tokens (every expert's rows, including the ragged last m-tiles), and bit-identical over two
+    runs (the fix-up's order is fixed)."""
+    T, H, E, K, I = 8192, 2048, 16, 2, 512
+    assert ffn_schedule(T, H, E, K, I) == 1
+    rng = np.random.default_rng(23)
+    x = rng.standard_normal((T, H)).astype(np.float16)
+    ew = np.concatenate([rng.standard_normal((E, 2 * I, H)) / math.sqrt(H),
+                         rng.standard_normal((E, I, H)) / math.sqrt(I)], axis=1).astype(np.float16)
+    ids = np.stack([rng.permutation(E)[:K] for _ in range(T)]).astype(np.int32)
+    w = np.full((T, K), 1.0 / K, np.float16)
+    x_d, ids_d, w_d, ew_d = dev(x), dev(ids), dev(w), dev(ew)
+    eo_d, ws = run_ffn(ops, x_d, ids_d, w_d, ew_d, I)
+    eo = host(eo_d)
+    eo2_d, _ = run_ffn(ops, x_d, ids_d, w_d, ew_d, I)
+    assert np.array_equal(eo.view(np.uint16), host(eo2_d).view(np.uint16)), "tiled FFN is not deterministic"
+    check_permute(host(ws[: 4 * (E + 1) + 256 + 4 * T * K]), ids, E)
+    # the last rows of each expert sit in its ragged m-tile; sample them and a spread of the rest
+    tok = set(np.linspace(0, T - 1, 128).astype(int).tolist())
+    for e in range(E):
+        tok.update(np.nonzero((ids == e).any(axis=1))[0][-4:].tolist())
+    tok = np.array(sorted(tok))
+    eo_o = oracle.expert_ffn(f32(x[tok]), ids[tok], f32(ew), I)
+    m = oracle.compare(f32(eo)[tok], eo_o)
+    log(f"[tiled split T{T} H{H} E{E} K{K} I{I}] expert_out vs oracle on {len(tok)} tokens: {m}")
+    within(m, max_abs=1e-2, mean_abs=1e-3, cos=0.9999)
+
+
 def test_decode_uses_streaming_and_prefill_uses_tiled():
     assert ffn_schedule(128, 2048, 16, 2, 8192) == 0
     assert ffn_schedule(8192, 2048, 16, 2, 8192) == 1
