@@ -52,6 +52,7 @@ constexpr int kNStage = 2;
 constexpr int kLdsBytes = kNStage * kStageHalfs * 2;  // the ring; the tile table follows it
 constexpr int kLdsMax = 160 * 1024;
 constexpr int kXcds = 8;
+constexpr int kCopyPolicy = 1;  // cache-policy bits of the stage copies: sc0
 // Partial tiles of the split leftover round: one fp32 kBM x kBN tile per workgroup of a persistent launch.
 constexpr int kMaxParts = 256;
 constexpr int kFixThreads = 256;
@@ -283,7 +284,9 @@ __global__ __launch_bounds__(kThreads) void ffn_tiled_kernel(TiledArgs p) {
                                                  static_cast<int>(3u * static_cast<uint32_t>(p.I) * p.H * 2), 0x00020000);
     };
 
-    // copies stage kc of plan P into ring slot q % 2
+    // copies stage kc of plan P into ring slot q % 2. The data is consumed from LDS, so the loads bypass the L1
+    // (sc0); they still allocate in L2, where the other m-tiles of the weight tile find them (a non-temporal hint
+    // there made the kernel 35 % slower).
     auto copy = [&](int q, int kc, const CopyPlan& P) __attribute__((always_inline)) {
         const int kb = kc * kBK * 2;  // byte offset of the stage along k (scalar)
         uint16_t* sa = lds + (q % kNStage) * kStageHalfs;
@@ -291,9 +294,9 @@ __global__ __launch_bounds__(kThreads) void ffn_tiled_kernel(TiledArgs p) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(P.ar, (__attribute__((address_space(3))) void*)(sa + (wave * 4 + j) * 8 * kPitch), 16,
-                                                     static_cast<int>(P.ao[j]), kb, 0, 0);
+                                                     static_cast<int>(P.ao[j]), kb, 0, kCopyPolicy);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(P.wr, (__attribute__((address_space(3))) void*)(sb + (wave * 4 + j) * 8 * kPitch), 16,
-                                                     static_cast<int>(P.bo[j]), kb, 0, 0);
+                                                     static_cast<int>(P.bo[j]), kb, 0, kCopyPolicy);
         }
     };
     f32x4 acc[8][4];
