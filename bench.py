@@ -20,7 +20,9 @@ W warm-up steps, then five timed passes of K steps each, every pass between torc
      `layer_us_per_step_events` (p10 / p50 / p90).
 Then two library kernels over 1 GiB give this box's achievable HBM rates next to the published 8 TB/s the
 roofline uses: a whole-line non-temporal streaming read (`hbm_read_gbps`, the access the decode weight stream
-uses) and a plain copy (`hbm_copy_gbps`, read + write). Kernels whose per-launch inputs fit the 256 MB Infinity
+uses) and a plain copy (`hbm_copy_gbps`, read + write); and the vendor library's dense fp16 GEMM (hipBLASLt
+through torch.matmul, 8192 x 8192 x 8192, A @ B^T) gives its achievable MFMA rate next to the published
+2.5 PFLOP/s (`gemm_fp16_tflops_library`). Kernels whose per-launch inputs fit the 256 MB Infinity
 Cache (routing and combine at decode) are flagged `cache_resident`: repeated steps read them from it.
 
 The JSON line also carries:
@@ -132,7 +134,8 @@ def main() -> int:
     ap.add_argument("--cpu-target-gflop", type=float, default=30.0,
                     help="size of the CPU baseline sample in GFLOP of expert FFN work")
     ap.add_argument("--no-graph", action="store_true", help="skip the HIP-graph replay timing")
-    ap.add_argument("--no-copy-rate", action="store_true", help="skip the 1 GiB read and copy rate measurements")
+    ap.add_argument("--no-copy-rate", action="store_true",
+                    help="skip the achievable-rate probes (1 GiB read and copy, library fp16 GEMM)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="instead of the layer, run moe_copy_bytes over MIB MiB (reference for HBM byte counters)")
     args = ap.parse_args()
@@ -272,6 +275,23 @@ def main() -> int:
         read_gbps = round(nb / (tot_ms / nl * 1e-3) / 1e9, 1)
         del src
         progress(f"1 GiB: copy kernel {copy_gbps} GB/s (read + write), streaming read {read_gbps} GB/s")
+    # 7) achievable dense fp16 MFMA rate on this box: the vendor library's GEMM on a large square problem
+    gemm_tflops = None
+    if not args.no_copy_rate:
+        n = 8192
+        ga = torch.randn(n, n, device=dev, dtype=torch.float16)
+        gb = torch.randn(n, n, device=dev, dtype=torch.float16)
+        for _ in range(3):
+            gc = ga @ gb.t()
+        g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        g0.record()
+        for _ in range(10):
+            gc = ga @ gb.t()
+        g1.record()
+        torch.cuda.synchronize()
+        gemm_tflops = round(2 * n ** 3 / (g0.elapsed_time(g1) / 10 * 1e-3) / 1e12, 1)
+        del ga, gb, gc
+        progress(f"library fp16 GEMM {n}^3: {gemm_tflops} TFLOP/s")
 
     ids_h = ids.cpu().numpy()
     active = int((np.bincount(ids_h.ravel(), minlength=E) > 0).sum())
@@ -285,7 +305,8 @@ def main() -> int:
                             "TFLOP/s": round(f / (avg * 1e-3) / 1e12, 2) if f else None,
                             # inputs re-read every step that fit the 256 MB Infinity Cache are served from it
                             "cache_resident": bool(b) and b < MALL_BYTES}
-    ffn_names = ("moe_permute", "moe_ffn_gateup_swiglu", "moe_ffn_down", "moe_ffn_down_reduce")
+    ffn_names = ("moe_permute", "moe_ffn_gateup_swiglu", "moe_ffn_gateup_fixup", "moe_ffn_down", "moe_ffn_down_fixup",
+                 "moe_ffn_down_reduce")
     ffn_ms = sum(kernels[n][1] / kernels[n][0] for n in ffn_names if n in kernels)
     ffn_flops = 6 * T * K * H * I
     ffn_bytes = active * 3 * I * H * 2 + T * H * 2 + T * K * H * 2
@@ -360,6 +381,7 @@ def main() -> int:
         "kernels": per_kernel,
         "hbm_copy_gbps": copy_gbps,
         "hbm_read_gbps": read_gbps,
+        "gemm_fp16_tflops_library": gemm_tflops,
         "roofline": roofline,
         "cpu_baseline": cpu_baseline,
         "cpu_baseline_tiled": cpu_baseline_tiled,
