@@ -35,8 +35,8 @@ int ffn_schedule(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
 
 // Layout (each region 256-byte aligned): offsets [E+1] i32 | sorted_slot [T*K] i32 | hidden [T*K, I] fp16, then
 // for the weight-streaming schedule: partial [nsplit, T*K, H] fp32 (when the down projection is split over K) |
-// slot_row [T*K] i32; for the tiled schedule: partial tiles [256, 256, 256] fp32 (64 MiB) of the leftover
-// round it splits over k.
+// slot_row [T*K] i32; for the tiled schedule: up to 256 fp32 partial tiles of 256 x 256 (64 MiB; one per
+// workgroup of the down launch, none when I < 256) for the leftover round it splits over k.
 size_t ffn_workspace_bytes(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
     const size_t S = static_cast<size_t>(T) * static_cast<size_t>(K);
     size_t bytes = align_up(sizeof(int32_t) * static_cast<size_t>(E + 1), 256);
@@ -47,7 +47,8 @@ size_t ffn_workspace_bytes(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I
                                                static_cast<int>(I)), 256);
         bytes += align_up(sizeof(int32_t) * S, 256);
     } else if (ffn_schedule(T, H, E, K, I) == 1) {
-        bytes += align_up(tiled_partial_bytes(), 256);
+        bytes += align_up(tiled_partial_bytes(static_cast<int>(T), static_cast<int>(H), static_cast<int>(E),
+                                              static_cast<int>(K), static_cast<int>(I)), 256);
     }
     return bytes;
 }

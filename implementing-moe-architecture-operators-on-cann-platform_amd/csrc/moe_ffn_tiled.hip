@@ -586,7 +586,15 @@ bool tiled_supported(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
     return kLdsBytes + 8 * (E + 1) + 3 * kBM * 4 <= kLdsMax;
 }
 int tiled_block_threads() { return kThreads; }
-size_t tiled_partial_bytes() { return static_cast<size_t>(kMaxParts) * kBM * kBN * sizeof(float); }
+// The down projection splits leftover tiles into pieces of at least two k-stages (so only when I / kBK >= 4); a
+// piece writes the partial slot of its workgroup, and the launch has at most min(kMaxParts, tiled_down_grid)
+// workgroups.
+bool tiled_down_splits(int I) { return I / kBK >= 4; }
+size_t tiled_partial_bytes(int T, int H, int E, int K, int I) {
+    if (!tiled_down_splits(I)) return 0;
+    const int slots = min(kMaxParts, tiled_down_grid(T, E, K, H));
+    return static_cast<size_t>(slots) * kBM * kBN * sizeof(float);
+}
 int tiled_rows_per_tile() { return kBM; }
 // Upper bound on the tile count (sum over experts of ceil(rows_e / kBM) <= ceil(T*K / kBM) + E), rounded up to
 // a multiple of the XCD count so that the XCD-contiguous remap in the kernel is a bijection on [0, grid).
@@ -625,8 +633,8 @@ hipError_t launch_ffn_tiled(const uint16_t* x, const uint16_t* expert_weights, u
     p.ndim = H;
     p.ntiles_n = (H + kBN - 1) / kBN;
     p.gather = 0;
-    return launch_tiled<kScatter>(p, tiled_down_grid(T, E, K, H), true, true, "moe_ffn_down", "moe_ffn_down_fixup",
-                                  stream);
+    return launch_tiled<kScatter>(p, tiled_down_grid(T, E, K, H), true, tiled_down_splits(I), "moe_ffn_down",
+                                  "moe_ffn_down_fixup", stream);
 }
 
 }  // namespace moe

@@ -76,8 +76,8 @@ hipError_t launch_ffn_stream(const uint16_t* x, const int32_t* expert_ids, const
 // LDS-tiled schedule (moe_ffn_tiled.hip)
 bool tiled_supported(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I);
 int tiled_block_threads();
-// fp32 partial tiles of the split leftover round (workspace region after hidden)
-size_t tiled_partial_bytes();
+// fp32 partial tiles of the down projection's split leftover round (workspace region after hidden)
+size_t tiled_partial_bytes(int T, int H, int E, int K, int I);
 int tiled_rows_per_tile();
 int tiled_gateup_grid(int T, int E, int K, int I);
 int tiled_down_grid(int T, int E, int K, int H);

@@ -118,8 +118,8 @@ moe_status moe_expert_ffn_infer_dtype(moe_dtype* expert_out_dtype);
 
 /* Workspace bytes for one call (TilingFunc workspace, op_host/moe_ops.cpp:340-349). Holds the expert-sorted
  * slot order, per-expert offsets and the fp16 SwiGLU intermediate [T*K, I]; on the weight-streaming schedule
- * also the split-K partial sums and the slot -> sorted-row map; on the LDS-tiled schedule also 64 MiB of fp32
- * partial tiles for the tiles it splits over k. 0 for invalid sizes. */
+ * also the split-K partial sums and the slot -> sorted-row map; on the LDS-tiled schedule also up to 64 MiB of
+ * fp32 partial tiles for the tiles it splits over k. 0 for invalid sizes. */
 size_t moe_expert_ffn_workspace_bytes(int64_t num_tokens, int64_t hidden_size, int64_t num_experts,
                                       int64_t top_k, int64_t intermediate_size);
 
