@@ -18,12 +18,16 @@
 //                both pipes stay busy. One barrier per stage, between the third and the fourth phase: by then
 //                the wave has read all of stage q, and stage q + 1 has landed, so the barrier publishes q + 1
 //                and frees q's slot for the copies of q + 2.
-//   persistent   (gate/up) one workgroup per CU walks its tiles back to back and the ring runs on across
-//                them: the copies of a tile's first two stages go out during the previous tile's last two.
-//                The tile table (per-expert tile prefix and row offsets) is built once per workgroup in LDS, so
-//                finding a tile is a short LDS binary search; the next tile's 256 sorted-slot entries are copied
-//                into LDS a tile ahead. The down projection has ~2 tiles per CU, where the hardware's own
-//                dispatch balances better, so it runs one workgroup per tile through the same kernel.
+//   persistent   one workgroup per CU walks its tiles back to back and the ring runs on across them: the
+//                copies of a tile's first two stages go out during the previous tile's last two. The tile table
+//                (per-expert tile prefix and row offsets) is built once per workgroup in LDS, so finding a tile
+//                is a short LDS binary search; the next tile's 256 sorted-slot entries are copied into LDS a tile
+//                ahead.
+//   split        (down) the down projection has only ~2 tiles per CU at prefill, so a count-based schedule
+//                leaves the last round mostly idle: the tiles left over after the full rounds are split over k
+//                into pieces, one per workgroup, that write fp32 partial tiles; ffn_tiled_fixup_kernel adds them
+//                in piece order. The split is a separate instantiation (SPLIT), so gate/up keeps its register
+//                allocation at tile changes.
 //   LDS layout   unpadded 128-byte rows of 8 granules of 16 B; granule g of row r is stored at g ^ ((r >> 1) & 7),
 //                so the 16 rows one ds_read_b128 touches (same logical granule) spread over all banks
 //   gate/up      the 256 weight rows of a tile are, per wave quarter, 32 W_gate rows and the matching 32 W_up
@@ -440,12 +444,11 @@ __global__ __launch_bounds__(kThreads) void ffn_tiled_kernel(TiledArgs p) {
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // the surplus copies have landed before the workgroup ends
 }
 
-// Adds the pieces of each split leftover tile in piece order (fixed, so the result does not depend on timing) and
-// applies the tile's epilogue. Workgroup (g, rb) takes rows [rb * kFixRows, +kFixRows) of leftover tile
+// Down projection: adds the pieces of each split leftover tile in piece order (fixed, so the result does not
+// depend on timing) and scatters the fp16 rows to expert_out. Workgroup (g, rb) takes rows [rb * kFixRows, +kFixRows) of leftover tile
 // j = g / 8 of XCD x = g % 8; piece pc of that tile is in the partial slot of workgroup (j * S + pc) * 8 + x of the
 // tiled launch, whose grid had nloc workgroups per XCD. The tile is found as the tiled kernel finds it, from
 // offsets (each wave scans the experts 64 at a time).
-template <int EPI>
 __global__ __launch_bounds__(kFixThreads) void ffn_tiled_fixup_kernel(TiledArgs p, int nloc) {
     constexpr int nrb = kBM / kFixRows;
     const int rb = static_cast<int>(blockIdx.x) % nrb, g = static_cast<int>(blockIdx.x) / nrb;
@@ -488,89 +491,54 @@ __global__ __launch_bounds__(kFixThreads) void ffn_tiled_fixup_kernel(TiledArgs 
     const float* part0 = p.partial + static_cast<size_t>(j * xs.S * kXcds + x) * (kBM * kBN);
     const size_t pstride = static_cast<size_t>(kXcds) * (kBM * kBN);  // next piece: li + 1
     const int tid = static_cast<int>(threadIdx.x);
-    if (EPI == kScatter) {
-        // 64 threads per row, 4 consecutive output columns each; 4 rows per thread, loaded together
-        constexpr int kRows = kFixRows / (kFixThreads / 64);
-        const int c = (tid % 64) * 4, r0 = rb * kFixRows + tid / 64;
-        const float* src = part0 + r0 * kBN + c;
-        f32x4 v[kRows];
+    // 64 threads per row, 4 consecutive output columns each; 4 rows per thread, loaded together
+    constexpr int kRows = kFixRows / (kFixThreads / 64);
+    const int c = (tid % 64) * 4, r0 = rb * kFixRows + tid / 64;
+    const float* src = part0 + r0 * kBN + c;
+    f32x4 v[kRows];
 #pragma unroll
-        for (int u = 0; u < kRows; ++u) v[u] = *reinterpret_cast<const f32x4*>(src + u * (kFixThreads / 64) * kBN);
+    for (int u = 0; u < kRows; ++u) v[u] = *reinterpret_cast<const f32x4*>(src + u * (kFixThreads / 64) * kBN);
 #pragma unroll 2
-        for (int pc = 1; pc < xs.S; ++pc)
+    for (int pc = 1; pc < xs.S; ++pc)
 #pragma unroll
-            for (int u = 0; u < kRows; ++u)
-                v[u] += *reinterpret_cast<const f32x4*>(src + pc * pstride + u * (kFixThreads / 64) * kBN);
-        const int col = nt * kBN + c;
+        for (int u = 0; u < kRows; ++u)
+            v[u] += *reinterpret_cast<const f32x4*>(src + pc * pstride + u * (kFixThreads / 64) * kBN);
+    const int col = nt * kBN + c;
 #pragma unroll
-        for (int u = 0; u < kRows; ++u) {
-            const int r = r0 + u * (kFixThreads / 64);
-            if (r >= rows || col >= p.H) continue;
-            const uint32_t lo = f32_to_f16_bits(v[u][0]) | (static_cast<uint32_t>(f32_to_f16_bits(v[u][1])) << 16);
-            const uint32_t hi = f32_to_f16_bits(v[u][2]) | (static_cast<uint32_t>(f32_to_f16_bits(v[u][3])) << 16);
-            const int slot = p.sorted_slot[off + mt * kBM + r];
-            *reinterpret_cast<uint2*>(p.out + static_cast<size_t>(slot) * p.H + col) = make_uint2(lo, hi);
-        }
-    } else {
-        // 32 threads per row, 4 consecutive hidden columns each; hidden column hc of the tile is weight-row column
-        // (hc / 32) * 64 + hc % 32 (gate) and 32 past it (up); 2 rows per thread, loaded together
-        constexpr int kRows = kFixRows / (kFixThreads / 32);
-        const int hc = (tid % 32) * 4, r0 = rb * kFixRows + tid / 32;
-        const float* src = part0 + r0 * kBN + (hc / 32) * 64 + hc % 32;
-        f32x4 gv[kRows], uv[kRows];
-#pragma unroll
-        for (int u = 0; u < kRows; ++u) {
-            gv[u] = *reinterpret_cast<const f32x4*>(src + u * (kFixThreads / 32) * kBN);
-            uv[u] = *reinterpret_cast<const f32x4*>(src + u * (kFixThreads / 32) * kBN + 32);
-        }
-#pragma unroll 2
-        for (int pc = 1; pc < xs.S; ++pc)
-#pragma unroll
-            for (int u = 0; u < kRows; ++u) {
-                gv[u] += *reinterpret_cast<const f32x4*>(src + pc * pstride + u * (kFixThreads / 32) * kBN);
-                uv[u] += *reinterpret_cast<const f32x4*>(src + pc * pstride + u * (kFixThreads / 32) * kBN + 32);
-            }
-        const int col = nt * 128 + hc;
-#pragma unroll
-        for (int u = 0; u < kRows; ++u) {
-            const int r = r0 + u * (kFixThreads / 32);
-            if (r >= rows || col >= p.I) continue;
-            const uint32_t lo = f32_to_f16_bits(swiglu_fast(gv[u][0], uv[u][0])) |
-                                (static_cast<uint32_t>(f32_to_f16_bits(swiglu_fast(gv[u][1], uv[u][1]))) << 16);
-            const uint32_t hi = f32_to_f16_bits(swiglu_fast(gv[u][2], uv[u][2])) |
-                                (static_cast<uint32_t>(f32_to_f16_bits(swiglu_fast(gv[u][3], uv[u][3]))) << 16);
-            *reinterpret_cast<uint2*>(p.out + static_cast<size_t>(off + mt * kBM + r) * p.I + col) = make_uint2(lo, hi);
-        }
+    for (int u = 0; u < kRows; ++u) {
+        const int r = r0 + u * (kFixThreads / 64);
+        if (r >= rows || col >= p.H) continue;
+        const uint32_t lo = f32_to_f16_bits(v[u][0]) | (static_cast<uint32_t>(f32_to_f16_bits(v[u][1])) << 16);
+        const uint32_t hi = f32_to_f16_bits(v[u][2]) | (static_cast<uint32_t>(f32_to_f16_bits(v[u][3])) << 16);
+        const int slot = p.sorted_slot[off + mt * kBM + r];
+        *reinterpret_cast<uint2*>(p.out + static_cast<size_t>(slot) * p.H + col) = make_uint2(lo, hi);
     }
 }
 
-// use_split: persistent grid with the leftover tiles split over k, then the fix-up kernel
-template <int EPI>
-hipError_t launch_tiled(TiledArgs p, int grid, bool persistent, bool use_split, const char* name,
-                        const char* fix_name, hipStream_t stream) {
-    const void* fn = use_split ? reinterpret_cast<const void*>(&ffn_tiled_kernel<EPI, true>)
-                               : reinterpret_cast<const void*>(&ffn_tiled_kernel<EPI, false>);
+// Persistent grid: at most the workgroups the device holds at once, a multiple of the XCD count. SPLIT (the down
+// projection): with p.split set, the leftover tiles are split over k and the fix-up kernel follows.
+template <int EPI, bool SPLIT>
+hipError_t launch_tiled(TiledArgs p, int grid, const char* name, hipStream_t stream) {
+    const void* fn = reinterpret_cast<const void*>(&ffn_tiled_kernel<EPI, SPLIT>);
     const hipError_t attr = ensure_lds_limit(fn, kLdsMax);
     if (attr != hipSuccess) return attr;
     const int lds = kLdsBytes + 8 * (p.E + 1) + 3 * kBM * 4;
-    // persistent: at most the workgroups the device holds at once, a multiple of the XCD count
     const int resident = resident_workgroups(fn, kThreads, lds);
-    if (persistent && resident > 0 && resident < grid) grid = resident;
+    if (resident > 0 && resident < grid) grid = resident;
     grid = grid / kXcds * kXcds;
     if (grid < kXcds) grid = kXcds;
-    // a split needs the persistent grid (the leftover round is sized by the workgroups per XCD) and one partial
-    // slot per workgroup
-    p.split = (use_split && persistent && resident > 0 && grid <= resident && grid <= kMaxParts) ? 1 : 0;
+    // the leftover round is sized by the workgroups per XCD, so a split needs the grid to be all resident; each
+    // workgroup owns one partial slot
+    p.split = (SPLIT && p.split && resident > 0 && grid <= kMaxParts) ? 1 : 0;
     {
         TraceScope trace(name, stream);
-        if (use_split) ffn_tiled_kernel<EPI, true><<<grid, kThreads, lds, stream>>>(p);
-        else ffn_tiled_kernel<EPI, false><<<grid, kThreads, lds, stream>>>(p);
+        ffn_tiled_kernel<EPI, SPLIT><<<grid, kThreads, lds, stream>>>(p);
     }
     hipError_t err = hipGetLastError();
     if (err != hipSuccess || !p.split) return err;
     {
-        TraceScope trace(fix_name, stream);
-        ffn_tiled_fixup_kernel<EPI><<<grid * (kBM / kFixRows), kFixThreads, 0, stream>>>(p, grid / kXcds);
+        TraceScope trace("moe_ffn_down_fixup", stream);
+        ffn_tiled_fixup_kernel<<<grid * (kBM / kFixRows), kFixThreads, 0, stream>>>(p, grid / kXcds);
     }
     return hipGetLastError();
 }
@@ -624,8 +592,8 @@ hipError_t launch_ffn_tiled(const uint16_t* x, const uint16_t* expert_weights, u
     p.ntiles_n = (I + 127) / 128;
     p.gather = 1;
     p.partial = ws.partial;
-    const hipError_t err = launch_tiled<kSwiGLU>(p, tiled_gateup_grid(T, E, K, I), true, false,
-                                                 "moe_ffn_gateup_swiglu", "moe_ffn_gateup_fixup", stream);
+    const hipError_t err = launch_tiled<kSwiGLU, false>(p, tiled_gateup_grid(T, E, K, I), "moe_ffn_gateup_swiglu",
+                                                        stream);
     if (err != hipSuccess) return err;
     p.act = ws.hidden;
     p.out = expert_out;
@@ -633,8 +601,8 @@ hipError_t launch_ffn_tiled(const uint16_t* x, const uint16_t* expert_weights, u
     p.ndim = H;
     p.ntiles_n = (H + kBN - 1) / kBN;
     p.gather = 0;
-    return launch_tiled<kScatter>(p, tiled_down_grid(T, E, K, H), true, tiled_down_splits(I), "moe_ffn_down",
-                                  "moe_ffn_down_fixup", stream);
+    p.split = tiled_down_splits(I) ? 1 : 0;
+    return launch_tiled<kScatter, true>(p, tiled_down_grid(T, E, K, H), "moe_ffn_down", stream);
 }
 
 }  // namespace moe
