@@ -9,8 +9,8 @@ A step is one pass of the layer over one batch of synthetic input resident in HB
 through the C ABI of libmoe_mi355x.so on one stream, with caller-owned buffers allocated once.
 W warm-up steps, then five timed passes of K steps each, every pass between torch.cuda.synchronize() calls:
   1. eager: the three C-ABI calls per step, nothing else recorded -> `value` and `ms_per_step`;
-  2. graph replay: the same three calls captured once in a HIP graph, replayed K times (y checked bit-exact
-     against the eager y first) -> `layer_us_graph_replay`;
+  2. graph replay: the same three calls captured once in a HIP graph, replayed W times untimed and then K times
+     (y checked bit-exact against the eager y first) -> `layer_us_graph_replay`;
   3. traced: eager again, with HIP events that the library records around each of its launches on the launch
      stream -> per-kernel average durations, from which `roofline` is computed.
   4. fused: routing, then moe_expert_ffn_combine (the FFN and the combine in one call, an optional fast path;
@@ -216,6 +216,10 @@ def main() -> int:
         torch.cuda.synchronize()
         if not torch.equal(y, y_eager):
             raise RuntimeError("graph replay of the layer differs from the eager layer")
+        # as many untimed replays as the eager pass had warm-up steps: after the capture and the synchronisations
+        # the shader clock has dropped, and it takes ~15 launches of the prefill GEMMs to ramp back up
+        for _ in range(args.warmup):
+            g.replay()
         graph_ms, _ = timed(g.replay)
         progress(f"graph replay: {graph_ms * 1e3:.1f} us/step (host clock)")
         del g
