@@ -456,6 +456,27 @@ def test_ffn_tiled_schedule_full_oracle(ops, T, H, E, K, I):
     within(m, max_abs=1e-2, mean_abs=1e-3, cos=0.9999)
 
 
+def test_ffn_tiled_unaligned_expert_ids(ops):
+    """expert_ids 4-byte but not 16-byte aligned (rows 1.. of a [T + 1, K] buffer; the C ABI does not require
+    more): expert_out equals the aligned call bit for bit and the permutation is stable."""
+    T, H, E, K, I = 600, 128, 8, 3, 128
+    assert ffn_schedule(T, H, E, K, I) == 1
+    rng = np.random.default_rng(31)
+    x = rng.standard_normal((T, H)).astype(np.float16)
+    ew = np.concatenate([rng.standard_normal((E, 2 * I, H)) / math.sqrt(H),
+                         rng.standard_normal((E, I, H)) / math.sqrt(I)], axis=1).astype(np.float16)
+    ids = np.stack([rng.permutation(E)[:K] for _ in range(T)]).astype(np.int32)
+    w = np.full((T, K), 1.0 / K, np.float16)
+    buf = dev(np.concatenate([np.zeros((1, K), np.int32), ids]))
+    ids_unaligned = buf[1:]
+    assert ids_unaligned.is_contiguous() and ids_unaligned.data_ptr() % 16 != 0
+    x_d, w_d, ew_d = dev(x), dev(w), dev(ew)
+    eo_u, ws_u = run_ffn(ops, x_d, ids_unaligned, w_d, ew_d, I)
+    eo_a, _ = run_ffn(ops, x_d, dev(ids), w_d, ew_d, I)
+    check_permute(host(ws_u), ids, E)
+    assert np.array_equal(host(eo_u).view(np.uint16), host(eo_a).view(np.uint16))
+
+
 def test_ffn_tiled_several_tiles_per_workgroup(ops):
     """512 gate/up tiles on a grid of at most one workgroup per CU: each workgroup runs several tiles with the
     copy ring running on from one tile into the next (other experts, other n-tiles). Checked against the oracle
