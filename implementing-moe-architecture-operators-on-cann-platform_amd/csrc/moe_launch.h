@@ -31,9 +31,9 @@ int resident_workgroups(const void* fn, int threads, size_t lds);
 
 // ---- routing (moe_routing.hip) ----
 int routing_expert_blocks(int E);
-int routing_tokens_per_block(int E);
-int routing_block_threads(int E);
-int routing_lds_bytes(int E);
+int routing_tokens_per_block(int T, int E);
+int routing_block_threads(int T, int E);
+int routing_lds_bytes(int T, int E);
 hipError_t launch_routing_topk(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H,
                                int E, int K, hipStream_t stream);
 

@@ -3,7 +3,10 @@
 // Reference: op_kernel/moe_routing.cpp (ComputeGate :238-254, SoftmaxRows :263-298, TopKSelect :304-369) and
 // the CPU oracle NaiveMoE steps 1-3, tests/moe_cpu_sim.cpp:198-243.
 //
-// One workgroup owns 16 tokens; W waves (16 when E <= 32, else 4, bounded by the LDS of the partials).
+// One workgroup owns 16 TB tokens (TB = 1, 2 or 4 blocks of 16, as many as keep >= 256 workgroups); W waves (16
+// when E <= 32, else 4, bounded by the LDS of the partials). Each w_gate fragment a wave loads (8 strided 2-byte
+// loads per lane) is multiplied into all TB token blocks: at T = 16384, E = 64 (TB = 4) that cut the kernel from
+// 80 to 51 us (events), at T = 8192, E = 16 (TB = 2) from 16.6 to 15.2 us.
 //   Phase 1: logits[16, E] = x[16, H] @ w_gate[H, E] on MFMA (v_mfma_f32_16x16x32_f16, fp32 accumulation;
 //            fp16 x fp16 products are exact in fp32). The H/32 k-steps are dealt round-robin to the W waves; a
 //            wave issues the loads of U k-steps before their MFMAs (at decode, H = 2048 and W = 16: all of a
@@ -34,9 +37,22 @@ namespace {
 
 constexpr int kTokensPerBlock = 16;
 
-constexpr int waves_for(int eb) { return eb <= 2 ? 16 : 4; }  // the narrow kernel runs E <= 64
-// k-steps whose loads are issued together (E <= 32 runs 1024 threads: 128 VGPRs per lane; E <= 64 256)
-constexpr int unroll_for(int eb) { return eb == 1 ? 4 : eb == 2 ? 2 : 4; }
+// The narrow kernel runs E <= 64. The wave count fixes each token's summation order (wave w adds the k-steps
+// w, w + W, ... and the partials are folded in wave order), so it does not depend on the token blocks: a token's
+// ids and weights are the same whatever T is. 8 waves at E = 64, T = 16384 were 5 % faster (48.9 against 51.3 us)
+// but would make the bits depend on T.
+constexpr int waves_for(int eb, int /*tb*/) { return eb <= 2 ? 16 : 4; }
+// k-steps whose loads are issued together (E <= 32 runs 1024 threads: 128 VGPRs per lane; E <= 64 256), for tb
+// 16-token blocks per workgroup
+constexpr int unroll_for(int eb, int tb) {
+    return tb == 1 ? (eb == 1 ? 4 : eb == 2 ? 2 : 4) : eb == 1 ? (tb == 2 ? 4 : 2) : eb == 2 ? (tb == 2 ? 2 : 1) : 2;
+}
+// 16-token blocks per workgroup of the narrow kernel: each w_gate fragment a wave loads feeds tb of them. As many
+// as keep the grid at >= 256 workgroups (one per CU).
+int narrow_token_blocks(int T) { return T >= 16 * 4 * 256 ? 4 : T >= 16 * 2 * 256 ? 2 : 1; }
+constexpr size_t narrow_lds_bytes(int eb, int tb) {
+    return static_cast<size_t>(waves_for(eb, tb)) * 16 * tb * eb * 16 * sizeof(float);
+}
 
 // softmax + top-K + renormalisation of one token's logits L[0..E) held in registers (Epad = EB * 16 >= E)
 template <int Epad>
@@ -109,43 +125,54 @@ __device__ __forceinline__ void select_lds(float* L, float* picked, int E, int K
     for (int k = 0; k < K; ++k) w_out[k] = f32_to_f16_bits(picked[k] / sel);
 }
 
-// EB = number of 16-expert blocks held in registers (ceil(E / 16) rounded up to an instantiated size).
-template <int EB>
-__global__ __launch_bounds__(waves_for(EB) * kWave) void routing_topk_kernel(const uint16_t* __restrict__ x,
+// EB = number of 16-expert blocks held in registers (ceil(E / 16) rounded up to an instantiated size); TB = 16-token
+// blocks per workgroup (every w_gate fragment a wave loads is multiplied into all TB of them).
+template <int EB, int TB>
+__global__ __launch_bounds__(waves_for(EB, TB) * kWave) void routing_topk_kernel(const uint16_t* __restrict__ x,
                                                                               const uint16_t* __restrict__ w_gate,
                                                                               int32_t* __restrict__ expert_ids,
                                                                               uint16_t* __restrict__ weights, int T,
                                                                               int H, int E, int K) {
-    constexpr int W = waves_for(EB);
-    constexpr int U = unroll_for(EB);
+    constexpr int W = waves_for(EB, TB);
+    constexpr int U = unroll_for(EB, TB);
     constexpr int Epad = EB * 16;
-    extern __shared__ float part[];  // [W][16 tokens][Epad] fp32 partial logits; row (0, t) receives the fold
+    constexpr int NT = 16 * TB;  // tokens per workgroup
+    extern __shared__ float part[];  // [W][NT tokens][Epad] fp32 partial logits; row (0, t) receives the fold
     const int lane = lane_id();
     const int wave = static_cast<int>(threadIdx.x) / kWave;
     const int row = lane & 15;  // A row (token) / B column (expert) owned by this lane
     const int kg = lane >> 4;   // k-group: 8 consecutive k of each 32-wide k-step
-    const int t0 = static_cast<int>(blockIdx.x) * kTokensPerBlock;
+    const int t0 = static_cast<int>(blockIdx.x) * NT;
 
     // ---- phase 1: partial logits on MFMA ----
-    const int tok = min(t0 + row, T - 1);  // rows past T read a valid row; their results are dropped
-    const uint16_t* xrow = x + static_cast<size_t>(tok) * H + kg * 8;
-    f32x4 acc[EB];
+    const uint16_t* xrow[TB];
 #pragma unroll
-    for (int b = 0; b < EB; ++b) acc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int tb = 0; tb < TB; ++tb) {
+        const int tok = min(t0 + tb * 16 + row, T - 1);  // rows past T read a valid row; their results are dropped
+        xrow[tb] = x + static_cast<size_t>(tok) * H + kg * 8;
+    }
+    f32x4 acc[TB][EB];
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+        for (int b = 0; b < EB; ++b) acc[tb][b] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     const int nsteps = H / 32;
     for (int s0 = wave; s0 < nsteps; s0 += U * W) {
-        f16x8 a[U];
+        f16x8 a[U][TB];
         f16x8 bv[U][EB];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int s = s0 + u * W;
             const bool in = s < nsteps;
             const int k0 = (in ? s : 0) * 32;
-            a[u] = load_f16x8(xrow + k0);
-            if (!in) {  // a k-step past H contributes nothing, whatever x holds (0 * inf would be NaN)
 #pragma unroll
-                for (int q = 0; q < 8; ++q) a[u][q] = static_cast<f16>(0.0f);
+            for (int tb = 0; tb < TB; ++tb) {
+                a[u][tb] = load_f16x8(xrow[tb] + k0);
+                if (!in) {  // a k-step past H contributes nothing, whatever x holds (0 * inf would be NaN)
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) a[u][tb][q] = static_cast<f16>(0.0f);
+                }
             }
             const uint16_t* wrow = w_gate + static_cast<size_t>(k0 + kg * 8) * E;
 #pragma unroll
@@ -160,26 +187,30 @@ __global__ __launch_bounds__(waves_for(EB) * kWave) void routing_topk_kernel(con
 #pragma unroll
         for (int u = 0; u < U; ++u)
 #pragma unroll
-            for (int b = 0; b < EB; ++b) acc[b] = mfma16x16x32(a[u], bv[u][b], acc[b]);
+            for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+                for (int b = 0; b < EB; ++b) acc[tb][b] = mfma16x16x32(a[u][tb], bv[u][b], acc[tb][b]);
     }
-    // D[token 4*kg + r][expert b*16 + row]
+    // D[token tb*16 + 4*kg + r][expert b*16 + row]
 #pragma unroll
-    for (int b = 0; b < EB; ++b)
+    for (int tb = 0; tb < TB; ++tb)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) part[(wave * 16 + kg * 4 + r) * Epad + b * 16 + row] = acc[b][r];
+        for (int b = 0; b < EB; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) part[(wave * NT + tb * 16 + kg * 4 + r) * Epad + b * 16 + row] = acc[tb][b][r];
     __syncthreads();
 
     // ---- fold: partial of wave 0 + wave 1 + ... in wave order, into the wave-0 rows ----
-    for (int i = static_cast<int>(threadIdx.x); i < 16 * Epad; i += W * kWave) {
+    for (int i = static_cast<int>(threadIdx.x); i < NT * Epad; i += W * kWave) {
         float v = part[i];
 #pragma unroll
-        for (int w = 1; w < W; ++w) v += part[w * 16 * Epad + i];
+        for (int w = 1; w < W; ++w) v += part[w * NT * Epad + i];
         part[i] = v;
     }
     __syncthreads();
 
     // ---- phase 2: one lane per token ----
-    if (threadIdx.x >= kTokensPerBlock) return;
+    if (threadIdx.x >= NT) return;
     const int t = static_cast<int>(threadIdx.x);
     if (t0 + t >= T) return;
     int32_t* ids_out = expert_ids + static_cast<size_t>(t0 + t) * K;
@@ -192,9 +223,9 @@ __global__ __launch_bounds__(waves_for(EB) * kWave) void routing_topk_kernel(con
 #pragma unroll
             for (int j = 0; j < 4; ++j) L[e + j] = v[j];
         }
-        select_registers<Epad>(L, part + (16 + t) * Epad, E, K, ids_out, w_out);  // K <= E <= Epad
+        select_registers<Epad>(L, part + (NT + t) * Epad, E, K, ids_out, w_out);  // K <= E <= Epad
     } else {
-        select_lds(part + t * Epad, part + (16 + t) * Epad, E, K, ids_out, w_out);  // wave-1 rows are free now
+        select_lds(part + t * Epad, part + (NT + t) * Epad, E, K, ids_out, w_out);  // wave-1 rows are free now
     }
 }
 
@@ -338,14 +369,27 @@ hipError_t launch_wide(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, 
     return hipGetLastError();
 }
 
+template <int EB, int TB>
+hipError_t launch_narrow(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H, int E,
+                         int K, hipStream_t stream) {
+    const int grid = (T + 16 * TB - 1) / (16 * TB);
+    const size_t lds = narrow_lds_bytes(EB, TB);
+    const hipError_t attr = ensure_lds_limit(reinterpret_cast<const void*>(&routing_topk_kernel<EB, TB>),
+                                             static_cast<int>(lds));
+    if (attr != hipSuccess) return attr;
+    TraceScope trace("moe_routing_topk", stream);
+    routing_topk_kernel<EB, TB><<<grid, waves_for(EB, TB) * kWave, lds, stream>>>(x, w_gate, ids, w, T, H, E, K);
+    return hipGetLastError();
+}
+
 template <int EB>
 hipError_t launch_eb(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H, int E,
                      int K, hipStream_t stream) {
-    const int grid = (T + kTokensPerBlock - 1) / kTokensPerBlock;
-    const size_t lds = static_cast<size_t>(waves_for(EB)) * 16 * EB * 16 * sizeof(float);
-    TraceScope trace("moe_routing_topk", stream);
-    routing_topk_kernel<EB><<<grid, waves_for(EB) * kWave, lds, stream>>>(x, w_gate, ids, w, T, H, E, K);
-    return hipGetLastError();
+    switch (narrow_token_blocks(T)) {
+        case 1: return launch_narrow<EB, 1>(x, w_gate, ids, w, T, H, E, K, stream);
+        case 2: return launch_narrow<EB, 2>(x, w_gate, ids, w, T, H, E, K, stream);
+        default: return launch_narrow<EB, 4>(x, w_gate, ids, w, T, H, E, K, stream);
+    }
 }
 
 }  // namespace
@@ -359,15 +403,17 @@ int routing_expert_blocks(int E) {
     return 16;
 }
 
-int routing_tokens_per_block(int E) { return routing_expert_blocks(E) <= 4 ? kTokensPerBlock : kWideTokens; }
-int routing_block_threads(int E) {
-    const int eb = routing_expert_blocks(E);
-    return eb <= 4 ? waves_for(eb) * kWave : kWideWaves * kWave;
+int routing_tokens_per_block(int T, int E) {
+    return routing_expert_blocks(E) <= 4 ? kTokensPerBlock * narrow_token_blocks(T) : kWideTokens;
 }
-int routing_lds_bytes(int E) {
+int routing_block_threads(int T, int E) {
+    const int eb = routing_expert_blocks(E);
+    return eb <= 4 ? waves_for(eb, narrow_token_blocks(T)) * kWave : kWideWaves * kWave;
+}
+int routing_lds_bytes(int T, int E) {
     const int eb = routing_expert_blocks(E);
     if (eb > 4) return static_cast<int>(wide_lds_bytes(eb));
-    return waves_for(eb) * 16 * eb * 16 * static_cast<int>(sizeof(float));
+    return static_cast<int>(narrow_lds_bytes(eb, narrow_token_blocks(T)));
 }
 
 hipError_t launch_routing_topk(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H,

@@ -204,13 +204,29 @@ def test_combine_k1_is_copy_and_equal_weights_mean(ops):
 
 
 @pytest.mark.parametrize("T,H,E,K", [(37, 64, 4, 2), (16, 96, 8, 8), (200, 256, 64, 6), (5, 32, 256, 32),
-                                     (1, 2048, 16, 2), (33, 128, 1, 1), (1000, 512, 130, 4)])
+                                     (1, 2048, 16, 2), (33, 128, 1, 1), (1000, 512, 130, 4),
+                                     # two and four 16-token blocks per workgroup, T not a multiple of them
+                                     (8200, 64, 20, 3), (16400, 96, 64, 6), (16384, 64, 8, 2)])
 def test_routing_shapes(ops, T, H, E, K):
     rng = np.random.default_rng(T * 1000 + E)
     x = rng.standard_normal((T, H)).astype(np.float16)
     wg = (rng.standard_normal((H, E)) / math.sqrt(H)).astype(np.float16)
     ids_d, w_d = ops.MoeRoutingTopK(dev(x), dev(wg), K)
     check_routing(host(ids_d), host(w_d), x, wg, K, f"routing T{T} H{H} E{E} K{K}")
+
+
+@pytest.mark.parametrize("E,K", [(16, 2), (64, 6)])
+def test_routing_is_batch_invariant(ops, E, K):
+    """A token's ids and weights do not depend on the batch it is routed in: 16400 tokens run 4 token blocks per
+    workgroup, their first 1000 alone run 1, and the rows agree bit for bit."""
+    T, H = 16400, 512
+    rng = np.random.default_rng(E)
+    x = rng.standard_normal((T, H)).astype(np.float16)
+    wg = (rng.standard_normal((H, E)) / math.sqrt(H)).astype(np.float16)
+    ids_all, w_all = ops.MoeRoutingTopK(dev(x), dev(wg), K)
+    ids_few, w_few = ops.MoeRoutingTopK(dev(x[:1000]), dev(wg), K)
+    assert np.array_equal(host(ids_all)[:1000], host(ids_few))
+    assert np.array_equal(host(w_all)[:1000].view(np.uint16), host(w_few).view(np.uint16))
 
 
 def test_routing_exact_ties_lowest_index_first(ops):
