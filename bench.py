@@ -14,7 +14,8 @@ W warm-up steps, then five timed passes of K steps each, every pass between torc
   3. traced: eager again, with HIP events that the library records around each of its launches on the launch
      stream -> per-kernel average durations, from which `roofline` is computed.
   4. fused: routing, then moe_expert_ffn_combine (the FFN and the combine in one call, an optional fast path;
-     expert_out and y checked bit-exact against the three-operator layer first) -> `layer_us_fused_ffn_combine`.
+     expert_out and y checked bit-exact against the three-operator layer first, then W untimed steps)
+     -> `layer_us_fused_ffn_combine`.
      `value` stays the three-operator layer, the drop-in pipeline.
   5. per-step events: the three-operator layer with an event pair around every step ->
      `layer_us_per_step_events` (p10 / p50 / p90).
@@ -242,6 +243,8 @@ def main() -> int:
     torch.cuda.synchronize()
     if not (torch.equal(y, y_eager) and torch.equal(eo, eo_eager)):
         raise RuntimeError("the fused FFN + combine differs from the three-operator layer")
+    for _ in range(args.warmup):  # the check above left the GPU idle: let the clock ramp up again
+        step_fused()
     fused_ms, fused_gpu_ms = timed(step_fused)
     progress(f"fused FFN + combine: {fused_ms * 1e3:.1f} us/step (host clock), {fused_gpu_ms * 1e3:.1f} us/step (events)")
     # 5) per-step spread of the three-operator layer: an event pair around every step
