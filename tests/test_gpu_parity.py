@@ -139,6 +139,31 @@ def test_moe_layer_chain_equals_stagewise(ops):
         assert torch.equal(a, b)  # deterministic: no atomics anywhere on the path
 
 
+def test_layer_empty_and_single_token(ops):
+    # T = 0: every operator and the fused path return empty outputs and launch nothing
+    H, E, K, I = 256, 8, 2, 512
+    rng = np.random.default_rng(11)
+    wg = (rng.standard_normal((H, E)) / math.sqrt(H)).astype(np.float16)
+    ew = np.concatenate([rng.standard_normal((E, 2 * I, H)) / math.sqrt(H),
+                         rng.standard_normal((E, I, H)) / math.sqrt(I)], axis=1).astype(np.float16)
+    wg_d, ew_d = dev(wg), dev(ew)
+    y0, ids0, w0, eo0 = ops.moe_layer(torch.empty(0, H, dtype=torch.float16, device="cuda"), wg_d, ew_d, K)
+    assert ids0.shape == (0, K) and w0.shape == (0, K) and eo0.shape == (0, K, H) and y0.shape == (0, H)
+    eo0f, y0f = ops.MoeExpertFFNCombine(torch.empty(0, H, dtype=torch.float16, device="cuda"), ids0, w0, ew_d)
+    assert eo0f.shape == (0, K, H) and y0f.shape == (0, H)
+    torch.cuda.synchronize()
+
+    # T = 1: one token through the whole layer against the oracle
+    x = rng.standard_normal((1, H)).astype(np.float16)
+    y_d, ids_d, w_d, eo_d = ops.moe_layer(dev(x), wg_d, ew_d, K)
+    ids, w = host(ids_d), host(w_d)
+    check_routing(ids, w, x, wg, K, "T=1")
+    eo = f32(host(eo_d))
+    within(oracle.compare(eo, oracle.expert_ffn(f32(x), ids, f32(ew), I)), max_abs=1e-2, mean_abs=1e-3, cos=0.9999)
+    y_o = oracle.combine(eo, f32(w)).astype(np.float16)
+    assert np.array_equal(host(y_d).view(np.uint16), y_o.view(np.uint16))
+
+
 @pytest.mark.parametrize("T,H,E,K,I,schedule", [(64, 256, 8, 2, 512, 0), (512, 256, 4, 2, 512, 1)])
 def test_layer_graph_replay_matches_eager(ops, T, H, E, K, I, schedule):
     """The layer's three C-ABI calls captured in one HIP graph: each replay, after eager work that changes x and
@@ -267,9 +292,9 @@ def test_ffn_edge_routings(ops):
     (1000, 64, 16, 1, 64, "uniform"),   # S = 1000: each wave's id scan runs several unrolled rounds
     (37, 128, 64, 3, 160, "invalid"),   # mostly empty experts, ids outside [0, E), I tail (160 = 5 x 32)
     # ring depths of the whole-line weight stream (D k-steps = D/2 column blocks of 64 k):
-    (64, 256, 8, 2, 512, "uniform"),    # gate/up D = 8, down D = 8 in one K-range (scatter epilogue)
+    (64, 256, 8, 2, 512, "uniform"),    # gate/up D = 8, down D = 4 in one K-range (scatter epilogue)
     (48, 128, 8, 2, 384, "uniform"),    # gate/up D = 4, down D = 4 in one K-range
-    (40, 512, 4, 2, 2560, "uniform"),   # down D = 8 over 2 K-ranges of 1280 (partials + reduce)
+    (40, 512, 4, 2, 2560, "uniform"),   # down D = 4 over 2 K-ranges of 1280 (partials + reduce)
 ])
 def test_ffn_streaming_schedule_edges(ops, T, H, E, K, I, pattern):
     """The weight-streaming schedule finds each expert's rows from expert_ids inside its gate/up kernel and
