@@ -560,8 +560,12 @@ template <int EPI>
 hipError_t launch_stream_epi(const StreamArgs& p, int d, int units, hipStream_t stream) {
     const size_t lds = static_cast<size_t>(p.rows_cap) * (p.kc + 8) * sizeof(uint16_t) + (d >= 2 ? kTbBytes : 0);
     hipError_t err = hipSuccess;
+    // pick_shape gives the down projection (kScatter, kPartial) a ring of at most 4 k-steps
+    constexpr int kMaxDepth = EPI == kSwiGLU ? 8 : 4;
 #define MOE_STREAM_CASE(DEPTH)                                                                                 \
     case DEPTH: {                                                                                              \
+        if constexpr (DEPTH > kMaxDepth) return hipErrorInvalidValue;                                           \
+        else {                                                                                                 \
         const void* fn = reinterpret_cast<const void*>(&ffn_stream_kernel<DEPTH, EPI>);                        \
         err = ensure_lds_limit(fn, kLdsMax);                                                                   \
         if (err != hipSuccess) return err;                                                                     \
@@ -569,6 +573,7 @@ hipError_t launch_stream_epi(const StreamArgs& p, int d, int units, hipStream_t 
         const int upw = slots > 0 ? (units + slots - 1) / slots : 1;                                          \
         ffn_stream_kernel<DEPTH, EPI><<<(units + upw - 1) / upw, kThreads, lds, stream>>>(p, upw);             \
         break;                                                                                                 \
+        }                                                                                                      \
     }
     switch (d) {
         MOE_STREAM_CASE(8)
