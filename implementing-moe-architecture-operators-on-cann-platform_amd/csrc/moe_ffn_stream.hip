@@ -538,7 +538,7 @@ __global__ __launch_bounds__(256) void reduce_combine_kernel(const float* __rest
 // K-range for one workgroup: the largest multiple of 32*D dividing kdim such that rows_cap rows of it (padded)
 // fit the LDS; deepest ring first. Sets kc, D, rows_cap. allow_split marks the down projection, whose ring is at
 // most 4 deep: at decode (I = 8192, 4 K-ranges of 2048) D = 4 runs it in 92.1-92.4 us against 93.6-94.0 us with
-// D = 8 (same box); gate/up keeps D = 8.
+// D = 8 and 93.7-93.9 us with D = 2 (same box each); gate/up keeps D = 8.
 struct StreamShape {
     int kc, d, rows_cap, nsplit;
 };
