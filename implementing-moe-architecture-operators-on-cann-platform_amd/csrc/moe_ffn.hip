@@ -26,34 +26,36 @@ constexpr int64_t kTiledMinRowsPerExpert = 64;
 
 int ffn_schedule(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
     const bool stream_ok = stream_supported(static_cast<int>(H), static_cast<int>(I));
-    const bool tiled_ok = tiled_supported(T, H, E, K, I);
     const bool many_rows = T * K >= kTiledMinRowsPerExpert * E;
-    if (tiled_ok && (many_rows || !stream_ok)) return 1;
+    if (tiled_shape_supported(H, E, I) && (many_rows || !stream_ok))
+        return tiled_size_supported(T, H, K, I) ? 1 : -1;
     if (stream_ok) return 0;
     return -1;
 }
 
 // Layout (each region 256-byte aligned): offsets [E+1] i32 | sorted_slot [T*K] i32 | hidden [T*K, I] fp16, then
 // for the weight-streaming schedule: partial [nsplit, T*K, H] fp32 (when the down projection is split over K) |
-// slot_row [T*K] i32; for the tiled schedule: up to 256 fp32 partial tiles of 256 x 256 (64 MiB; one per
-// workgroup of the down launch, none when I < 256) for the leftover round it splits over k.
-size_t ffn_workspace_bytes(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
+// slot_row [T*K] i32; for the tiled schedule with tiled_split: up to 256 fp32 partial tiles of 256 x 256 (64 MiB;
+// one per workgroup of the down launch, none when I < 256) for the leftover round it splits over k.
+size_t ffn_workspace_bytes(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I, bool tiled_split) {
     const size_t S = static_cast<size_t>(T) * static_cast<size_t>(K);
     size_t bytes = align_up(sizeof(int32_t) * static_cast<size_t>(E + 1), 256);
     bytes += align_up(sizeof(int32_t) * S, 256);
     bytes += align_up(sizeof(uint16_t) * S * static_cast<size_t>(I), 256);
-    if (ffn_schedule(T, H, E, K, I) == 0) {
+    const int schedule = ffn_schedule(T, H, E, K, I);
+    if (schedule == 0) {
         bytes += align_up(stream_partial_bytes(static_cast<int>(T), static_cast<int>(H), static_cast<int>(K),
                                                static_cast<int>(I)), 256);
         bytes += align_up(sizeof(int32_t) * S, 256);
-    } else if (ffn_schedule(T, H, E, K, I) == 1) {
+    } else if (schedule == 1 && tiled_split) {
         bytes += align_up(tiled_partial_bytes(static_cast<int>(T), static_cast<int>(H), static_cast<int>(E),
                                               static_cast<int>(K), static_cast<int>(I)), 256);
     }
     return bytes;
 }
 
-FfnWorkspace ffn_workspace_carve(void* base, int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
+FfnWorkspace ffn_workspace_carve(void* base, int64_t T, int64_t H, int64_t E, int64_t K, int64_t I,
+                                 bool tiled_split) {
     const size_t S = static_cast<size_t>(T) * static_cast<size_t>(K);
     char* p = static_cast<char*>(base);
     FfnWorkspace ws;
@@ -63,12 +65,18 @@ FfnWorkspace ffn_workspace_carve(void* base, int64_t T, int64_t H, int64_t E, in
     p += align_up(sizeof(int32_t) * S, 256);
     ws.hidden = reinterpret_cast<uint16_t*>(p);
     p += align_up(sizeof(uint16_t) * S * static_cast<size_t>(I), 256);
-    ws.partial = reinterpret_cast<float*>(p);
+    ws.partial = nullptr;
     ws.slot_row = nullptr;
-    if (ffn_schedule(T, H, E, K, I) == 0) {
+    const int schedule = ffn_schedule(T, H, E, K, I);
+    if (schedule == 0) {
+        ws.partial = reinterpret_cast<float*>(p);
         p += align_up(stream_partial_bytes(static_cast<int>(T), static_cast<int>(H), static_cast<int>(K),
                                            static_cast<int>(I)), 256);
         ws.slot_row = reinterpret_cast<int32_t*>(p);
+    } else if (schedule == 1 && tiled_split &&
+               tiled_partial_bytes(static_cast<int>(T), static_cast<int>(H), static_cast<int>(E),
+                                   static_cast<int>(K), static_cast<int>(I)) > 0) {
+        ws.partial = reinterpret_cast<float*>(p);
     }
     return ws;
 }
@@ -91,14 +99,21 @@ FfnGrid ffn_grid(int T, int H, int E, int K, int I) {
 }
 
 hipError_t launch_ffn(const uint16_t* x, const int32_t* expert_ids, const uint16_t* expert_weights,
-                      uint16_t* expert_out, FfnWorkspace ws, int T, int H, int E, int K, int I, hipStream_t stream) {
+                      uint16_t* expert_out, FfnWorkspace ws, int T, int H, int E, int K, int I, hipStream_t stream,
+                      bool tiled_split) {
     switch (ffn_schedule(T, H, E, K, I)) {
         case 1: {
-            const hipError_t err = launch_permute(expert_ids, T * K, E, H, ws, expert_out, stream);
+            hipError_t err = prepare_permute(T * K, E);
+            if (err == hipSuccess) err = prepare_ffn_tiled();
+            if (err == hipSuccess) err = launch_permute(expert_ids, T * K, E, H, ws, expert_out, stream);
             if (err != hipSuccess) return err;
-            return launch_ffn_tiled(x, expert_weights, expert_out, ws, T, H, E, K, I, stream);
+            return launch_ffn_tiled(x, expert_weights, expert_out, ws, T, H, E, K, I, stream, tiled_split);
         }
-        case 0: return launch_ffn_stream(x, expert_ids, expert_weights, expert_out, ws, T, H, E, K, I, stream);
+        case 0: {
+            const hipError_t err = prepare_ffn_stream(H, I);
+            if (err != hipSuccess) return err;
+            return launch_ffn_stream(x, expert_ids, expert_weights, expert_out, ws, T, H, E, K, I, stream);
+        }
         default: return hipErrorInvalidValue;
     }
 }
@@ -106,8 +121,11 @@ hipError_t launch_ffn(const uint16_t* x, const int32_t* expert_ids, const uint16
 hipError_t launch_ffn_combine(const uint16_t* x, const int32_t* expert_ids, const uint16_t* weights,
                               const uint16_t* expert_weights, uint16_t* expert_out, uint16_t* y, FfnWorkspace ws,
                               int T, int H, int E, int K, int I, hipStream_t stream) {
-    if (ffn_schedule(T, H, E, K, I) == 0)
+    if (ffn_schedule(T, H, E, K, I) == 0) {
+        const hipError_t err = prepare_ffn_stream(H, I);
+        if (err != hipSuccess) return err;
         return launch_ffn_stream(x, expert_ids, expert_weights, expert_out, ws, T, H, E, K, I, stream, weights, y);
+    }
     const hipError_t err = launch_ffn(x, expert_ids, expert_weights, expert_out, ws, T, H, E, K, I, stream);
     if (err != hipSuccess) return err;
     return launch_combine(expert_out, weights, y, T, H, K, stream);

@@ -587,7 +587,33 @@ hipError_t launch_stream_epi(const StreamArgs& p, int d, int units, hipStream_t 
     return err;
 }
 
+// The kernel instantiation launch_stream_epi runs for ring depth d (nullptr for none).
+template <int EPI>
+const void* stream_kernel_fn(int d) {
+    switch (d) {
+        case 8:
+            if constexpr (EPI == kSwiGLU) return reinterpret_cast<const void*>(&ffn_stream_kernel<8, EPI>);
+            else return nullptr;
+        case 4: return reinterpret_cast<const void*>(&ffn_stream_kernel<4, EPI>);
+        case 2: return reinterpret_cast<const void*>(&ffn_stream_kernel<2, EPI>);
+        case 1: return reinterpret_cast<const void*>(&ffn_stream_kernel<1, EPI>);
+        default: return nullptr;
+    }
+}
+
 }  // namespace
+
+hipError_t prepare_ffn_stream(int H, int I) {
+    const StreamShape gu = pick_shape(H, false), dn = pick_shape(I, true);
+    const void* fns[2] = {stream_kernel_fn<kSwiGLU>(gu.d),
+                          dn.nsplit > 1 ? stream_kernel_fn<kPartial>(dn.d) : stream_kernel_fn<kScatter>(dn.d)};
+    for (const void* fn : fns) {
+        if (!fn) return hipErrorInvalidValue;
+        const hipError_t err = ensure_lds_limit(fn, kLdsMax);
+        if (err != hipSuccess) return err;
+    }
+    return hipSuccess;
+}
 
 int stream_block_threads() { return kThreads; }
 int stream_rows_per_pass() { return kMaxRows; }

@@ -241,8 +241,8 @@ __global__ __launch_bounds__(kThreads) void ffn_tiled_kernel(TiledArgs p) {
     TileRef cur;
     if (!tile_at(0, cur)) return;
 
-    // activation rows a tile copies: gate/up gathers token rows, down reads its sorted hidden rows
-    const uint32_t act_rows = p.gather ? static_cast<uint32_t>(p.T) : static_cast<uint32_t>(p.offsets[p.E]);
+    // activation rows a tile copies: gate/up gathers token rows (x), down reads its own sorted hidden rows
+    const uint32_t act_rows = static_cast<uint32_t>(p.T);
     const uint32_t kbytes = static_cast<uint32_t>(p.kdim) * 2;
     const __amdgpu_buffer_rsrc_t srsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<int32_t*>(p.sorted_slot), 0,
                                                                           p.T * p.K * 4, 0x00020000);
@@ -278,10 +278,11 @@ __global__ __launch_bounds__(kThreads) void ffn_tiled_kernel(TiledArgs p) {
         }
         if (p.gather) {
             P.ar = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.act), 0, static_cast<int>(act_rows * kbytes), 0x00020000);
-        } else {
-            const uint32_t row0 = static_cast<uint32_t>(T.off + T.mt * kBM);
+        } else {  // the tile's own rows only: any T*K*I stays within 32-bit offsets
+            const int row0 = T.off + T.mt * kBM;
+            const int rows = min(kBM, T.ne - T.mt * kBM);
             P.ar = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.act + static_cast<size_t>(row0) * p.kdim), 0,
-                                                     static_cast<int>((act_rows - row0) * kbytes), 0x00020000);
+                                                     static_cast<int>(static_cast<uint32_t>(rows) * kbytes), 0x00020000);
         }
         const size_t ebase = static_cast<size_t>(T.e) * 3 * static_cast<size_t>(p.I) * p.H;
         P.wr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.w + ebase), 0,
@@ -520,8 +521,6 @@ __global__ __launch_bounds__(kFixThreads) void ffn_tiled_fixup_kernel(TiledArgs 
 template <int EPI, bool SPLIT>
 hipError_t launch_tiled(TiledArgs p, int grid, const char* name, hipStream_t stream) {
     const void* fn = reinterpret_cast<const void*>(&ffn_tiled_kernel<EPI, SPLIT>);
-    const hipError_t attr = ensure_lds_limit(fn, kLdsMax);
-    if (attr != hipSuccess) return attr;
     const int lds = kLdsBytes + 8 * (p.E + 1) + 3 * kBM * 4;
     const int resident = resident_workgroups(fn, kThreads, lds);
     if (resident > 0 && resident < grid) grid = resident;
@@ -545,13 +544,25 @@ hipError_t launch_tiled(TiledArgs p, int grid, const char* name, hipStream_t str
 
 }  // namespace
 
-// Both k extents need at least two stages (the ring runs two ahead); the buffer offsets are 32-bit; the tile
-// table must fit in the LDS left over by the ring.
-bool tiled_supported(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
+// Both k extents need at least two stages (the ring runs two ahead) and the tile table must fit in the LDS left
+// over by the ring.
+bool tiled_shape_supported(int64_t H, int64_t E, int64_t I) {
     if (H % kBK != 0 || I % kBK != 0 || H < 2 * kBK || I < 2 * kBK) return false;
-    const int64_t lim = int64_t(1) << 31;
-    if (T * H * 2 >= lim || T * K * I * 2 >= lim || 3 * I * H * 2 >= lim || T * K * 4 >= lim) return false;
     return kLdsBytes + 8 * (E + 1) + 3 * kBM * 4 <= kLdsMax;
+}
+// The buffer offsets are 32-bit: gathered x rows (T*H*2 bytes), one expert's weights (3*I*H*2) and the sorted
+// slots (T*K*4) must stay below 2 GiB. The down projection addresses hidden per tile, so T*K*I has no such bound.
+bool tiled_size_supported(int64_t T, int64_t H, int64_t K, int64_t I) {
+    const int64_t lim = int64_t(1) << 31;
+    return T * H * 2 < lim && 3 * I * H * 2 < lim && T * K * 4 < lim && static_cast<int64_t>(kBM) * I * 2 < lim;
+}
+bool tiled_supported(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
+    return tiled_shape_supported(H, E, I) && tiled_size_supported(T, H, K, I);
+}
+hipError_t prepare_ffn_tiled() {
+    hipError_t err = ensure_lds_limit(reinterpret_cast<const void*>(&ffn_tiled_kernel<kSwiGLU, false>), kLdsMax);
+    if (err != hipSuccess) return err;
+    return ensure_lds_limit(reinterpret_cast<const void*>(&ffn_tiled_kernel<kScatter, true>), kLdsMax);
 }
 int tiled_block_threads() { return kThreads; }
 // The down projection splits leftover tiles into pieces of at least two k-stages (so only when I / kBK >= 4); a
@@ -575,7 +586,8 @@ int tiled_gateup_grid(int T, int E, int K, int I) { return tiled_grid(T, E, K, (
 int tiled_down_grid(int T, int E, int K, int H) { return tiled_grid(T, E, K, (H + kBN - 1) / kBN); }
 
 hipError_t launch_ffn_tiled(const uint16_t* x, const uint16_t* expert_weights, uint16_t* expert_out,
-                            const FfnWorkspace& ws, int T, int H, int E, int K, int I, hipStream_t stream) {
+                            const FfnWorkspace& ws, int T, int H, int E, int K, int I, hipStream_t stream,
+                            bool allow_split) {
     TiledArgs p{};
     p.sorted_slot = ws.sorted_slot;
     p.offsets = ws.offsets;
@@ -601,7 +613,7 @@ hipError_t launch_ffn_tiled(const uint16_t* x, const uint16_t* expert_weights, u
     p.ndim = H;
     p.ntiles_n = (H + kBN - 1) / kBN;
     p.gather = 0;
-    p.split = tiled_down_splits(I) ? 1 : 0;
+    p.split = (allow_split && tiled_down_splits(I) && ws.partial != nullptr) ? 1 : 0;
     return launch_tiled<kScatter, true>(p, tiled_down_grid(T, E, K, H), "moe_ffn_down", stream);
 }
 

@@ -46,10 +46,13 @@ struct FfnWorkspace {
                            // tiled schedule's partial tiles of its split leftover round
     int32_t* slot_row;     // [T*K]   sorted row of each slot with a valid id (weight-streaming schedule only)
 };
-size_t ffn_workspace_bytes(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I);
-FfnWorkspace ffn_workspace_carve(void* base, int64_t T, int64_t H, int64_t E, int64_t K, int64_t I);
+// tiled_split = false leaves out the tiled schedule's partial tiles (its down projection then runs unsplit)
+size_t ffn_workspace_bytes(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I, bool tiled_split = true);
+FfnWorkspace ffn_workspace_carve(void* base, int64_t T, int64_t H, int64_t E, int64_t K, int64_t I,
+                                 bool tiled_split = true);
 
 int permute_block_threads();
+hipError_t prepare_permute(int S, int E);  // kernel attributes, before the first launch of a call
 hipError_t launch_permute(const int32_t* ids, int S, int E, int H, FfnWorkspace ws, uint16_t* expert_out,
                           hipStream_t stream);
 
@@ -65,6 +68,7 @@ FfnGrid ffn_grid(int T, int H, int E, int K, int I);
 int stream_block_threads();
 int stream_rows_per_pass();
 bool stream_supported(int H, int I);
+hipError_t prepare_ffn_stream(int H, int I);  // kernel attributes, before the first launch of a call
 size_t stream_partial_bytes(int T, int H, int K, int I);
 int stream_gateup_grid(int E, int H, int I);
 int stream_down_grid(int E, int H, int I);
@@ -74,20 +78,29 @@ hipError_t launch_ffn_stream(const uint16_t* x, const int32_t* expert_ids, const
                              uint16_t* expert_out, const FfnWorkspace& ws, int T, int H, int E, int K, int I,
                              hipStream_t stream, const uint16_t* weights = nullptr, uint16_t* y = nullptr);
 // LDS-tiled schedule (moe_ffn_tiled.hip)
+bool tiled_shape_supported(int64_t H, int64_t E, int64_t I);           // H, I granularity and LDS
+bool tiled_size_supported(int64_t T, int64_t H, int64_t K, int64_t I);  // 32-bit buffer offsets
 bool tiled_supported(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I);
+hipError_t prepare_ffn_tiled();  // kernel attributes, before the first launch of a call
 int tiled_block_threads();
 // fp32 partial tiles of the down projection's split leftover round (workspace region after hidden)
 size_t tiled_partial_bytes(int T, int H, int E, int K, int I);
 int tiled_rows_per_tile();
 int tiled_gateup_grid(int T, int E, int K, int I);
 int tiled_down_grid(int T, int E, int K, int H);
+// allow_split: the down projection may split its leftover tiles over k (needs ws.partial)
 hipError_t launch_ffn_tiled(const uint16_t* x, const uint16_t* expert_weights, uint16_t* expert_out,
-                            const FfnWorkspace& ws, int T, int H, int E, int K, int I, hipStream_t stream);
-// schedule choice: 0 = weight streaming, 1 = LDS-tiled, -1 = no kernel supports the shape
+                            const FfnWorkspace& ws, int T, int H, int E, int K, int I, hipStream_t stream,
+                            bool allow_split);
+// schedule choice: 0 = weight streaming, 1 = LDS-tiled, -1 = no kernel supports the shape. A shape with many rows
+// per expert that the tiled kernels support except for their 32-bit offsets is -1, not the streaming schedule
+// (which would re-stream every expert's weights once per 32 rows).
 int ffn_schedule(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I);
-// the whole FFN: permute (tiled schedule; the streaming schedule finds rows itself) and the two GEMMs
+// the whole FFN: permute (tiled schedule; the streaming schedule finds rows itself) and the two GEMMs. Every
+// kernel's attributes are set before the first launch, so a failure there leaves nothing launched.
 hipError_t launch_ffn(const uint16_t* x, const int32_t* expert_ids, const uint16_t* expert_weights,
-                      uint16_t* expert_out, FfnWorkspace ws, int T, int H, int E, int K, int I, hipStream_t stream);
+                      uint16_t* expert_out, FfnWorkspace ws, int T, int H, int E, int K, int I, hipStream_t stream,
+                      bool tiled_split = true);
 // the FFN followed by the combine: expert_out as launch_ffn writes it, y as launch_combine would compute it
 hipError_t launch_ffn_combine(const uint16_t* x, const int32_t* expert_ids, const uint16_t* weights,
                               const uint16_t* expert_weights, uint16_t* expert_out, uint16_t* y, FfnWorkspace ws,

@@ -59,9 +59,15 @@ moe_status check_ffn_sizes(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I
     if (st != MOE_OK) return st;
     if (I <= 0) return fail(MOE_ERR_ARG, "intermediateSize=%lld must be > 0", (long long)I);
     if (I % 32 != 0) return fail(MOE_ERR_UNSUPPORTED, "intermediateSize=%lld must be a multiple of 32", (long long)I);
-    if (moe::ffn_schedule(T, H, E, K, I) < 0)
+    if (moe::ffn_schedule(T, H, E, K, I) < 0) {
+        if (moe::tiled_shape_supported(H, E, I) && !moe::tiled_size_supported(T, H, K, I))
+            return fail(MOE_ERR_UNSUPPORTED,
+                        "T=%lld H=%lld K=%lld I=%lld exceeds the tiled expert GEMMs' 32-bit buffer offsets (x, one "
+                        "expert's weights and the sorted slots must each stay below 2 GiB)",
+                        (long long)T, (long long)H, (long long)K, (long long)I);
         return fail(MOE_ERR_UNSUPPORTED, "hiddenSize=%lld / intermediateSize=%lld: no expert GEMM schedule fits",
                     (long long)H, (long long)I);
+    }
     if (T * K * I > kInt32Max * 64LL) return fail(MOE_ERR_UNSUPPORTED, "T*K*I too large");
     return ok();
 }

@@ -127,6 +127,12 @@ __global__ __launch_bounds__(kPermuteWaves * kWave) void permute_kernel(const in
 
 int permute_block_threads() { return kPermuteWaves * kWave; }
 
+hipError_t prepare_permute(int S, int E) {
+    if (E <= 255 && S <= kPermuteLdsMax)
+        return ensure_lds_limit(reinterpret_cast<const void*>(&permute_kernel<true>), kPermuteLdsMax);
+    return hipSuccess;
+}
+
 hipError_t launch_permute(const int32_t* ids, int S, int E, int H, FfnWorkspace ws, uint16_t* expert_out,
                           hipStream_t stream) {
     TraceScope trace("moe_permute", stream);

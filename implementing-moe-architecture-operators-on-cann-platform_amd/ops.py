@@ -2,9 +2,11 @@
 
 Reference operator interface: op_host/moe_ops.cpp:537-679 (OpDef inputs/outputs/attrs) and the kernel
 entries op_kernel/moe_routing.cpp:434, op_kernel/moe_expert_ffn.cpp:613, op_kernel/moe_combine.cpp:136.
-Shapes and dtypes are inferred by the library (the InferShape/InferDataType replacements), outputs are
-allocated with torch on the input's device, and the launch is queued on torch's current stream. Errors
-raise MoeError with the library's message, before anything is launched.
+Shapes and dtypes are inferred by the library (the InferShape/InferDataType replacements), and the launch is
+queued on `stream` (torch's current stream when None). Outputs and any workspace the call allocates are
+allocated while that stream is current, so torch's caching allocator ties them to the stream the kernels run
+on: a workspace freed on return cannot be handed to other work before those kernels have finished with it.
+Errors raise MoeError with the library's message, before anything is launched.
 """
 from __future__ import annotations
 
@@ -19,9 +21,12 @@ from ._lib import MoeError, check, dims
 _TORCH_DT = {_lib.DT_FLOAT16: torch.float16, _lib.DT_INT32: torch.int32}
 
 
+def _stream(stream) -> "torch.cuda.Stream":
+    return stream if stream is not None else torch.cuda.current_stream()
+
+
 def _stream_ptr(stream) -> int:
-    s = stream if stream is not None else torch.cuda.current_stream()
-    return int(s.cuda_stream)
+    return int(_stream(stream).cuda_stream)
 
 
 def _need(t: torch.Tensor, name: str, dtype: torch.dtype) -> None:
@@ -79,11 +84,13 @@ def MoeRoutingTopK(x: torch.Tensor, w_gate: torch.Tensor, topK: int = 2, stream=
     _need(x, "x", torch.float16)
     _need(w_gate, "w_gate", torch.float16)
     (ids_shape, ids_dt), (w_shape, w_dt) = infer_routing(tuple(x.shape), tuple(w_gate.shape), topK)
-    ids = torch.empty(ids_shape, dtype=ids_dt, device=x.device)
-    w = torch.empty(w_shape, dtype=w_dt, device=x.device)
+    s = _stream(stream)
+    with torch.cuda.stream(s):
+        ids = torch.empty(ids_shape, dtype=ids_dt, device=x.device)
+        w = torch.empty(w_shape, dtype=w_dt, device=x.device)
     T, H = x.shape
     check(_lib.load().moe_routing_topk(x.data_ptr(), w_gate.data_ptr(), ids.data_ptr(), w.data_ptr(), T, H,
-                                       w_gate.shape[1], ids_shape[1], _stream_ptr(stream)))
+                                       w_gate.shape[1], ids_shape[1], int(s.cuda_stream)))
     return ids, w
 
 
@@ -99,13 +106,15 @@ def MoeExpertFFN(x: torch.Tensor, expert_ids: torch.Tensor, weights: torch.Tenso
     T, H = x.shape
     E, K = expert_weights.shape[0], expert_ids.shape[1]
     need = workspace_bytes(T, H, E, K, inter)
-    if workspace is None:
-        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
-    expert_out = torch.empty(out_shape, dtype=out_dt, device=x.device)
+    s = _stream(stream)
+    with torch.cuda.stream(s):
+        if workspace is None:
+            workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
+        expert_out = torch.empty(out_shape, dtype=out_dt, device=x.device)
     check(_lib.load().moe_expert_ffn(x.data_ptr(), expert_ids.data_ptr(), weights.data_ptr(),
                                      expert_weights.data_ptr(), expert_out.data_ptr(), workspace.data_ptr(),
                                      workspace.numel() * workspace.element_size(), T, H, E, K, inter,
-                                     _stream_ptr(stream)))
+                                     int(s.cuda_stream)))
     return expert_out
 
 
@@ -122,9 +131,11 @@ def MoeCombine(expert_out: torch.Tensor, expert_ids: torch.Tensor | None, weight
     T, K, H = expert_out.shape
     if tuple(weights.shape) != (T, K):
         raise MoeError(3, f"weights shape {tuple(weights.shape)} != {(T, K)}")
-    y = torch.empty(y_shape, dtype=y_dt, device=expert_out.device)
+    s = _stream(stream)
+    with torch.cuda.stream(s):
+        y = torch.empty(y_shape, dtype=y_dt, device=expert_out.device)
     check(_lib.load().moe_combine(expert_out.data_ptr(), _ptr(expert_ids), weights.data_ptr(), y.data_ptr(), T, H, K,
-                                  _stream_ptr(stream)))
+                                  int(s.cuda_stream)))
     return y
 
 
@@ -144,14 +155,16 @@ def MoeExpertFFNCombine(x: torch.Tensor, expert_ids: torch.Tensor, weights: torc
     if tuple(weights.shape) != (T, K):
         raise MoeError(3, f"weights shape {tuple(weights.shape)} != {(T, K)}")
     need = workspace_bytes(T, H, E, K, inter)
-    if workspace is None:
-        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
-    expert_out = torch.empty(out_shape, dtype=out_dt, device=x.device)
-    y = torch.empty((T, H), dtype=torch.float16, device=x.device)
+    s = _stream(stream)
+    with torch.cuda.stream(s):
+        if workspace is None:
+            workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
+        expert_out = torch.empty(out_shape, dtype=out_dt, device=x.device)
+        y = torch.empty((T, H), dtype=torch.float16, device=x.device)
     check(_lib.load().moe_expert_ffn_combine(x.data_ptr(), expert_ids.data_ptr(), weights.data_ptr(),
                                              expert_weights.data_ptr(), expert_out.data_ptr(), y.data_ptr(),
                                              workspace.data_ptr(), workspace.numel() * workspace.element_size(), T,
-                                             H, E, K, inter, _stream_ptr(stream)))
+                                             H, E, K, inter, int(s.cuda_stream)))
     return expert_out, y
 
 
@@ -159,9 +172,9 @@ def moe_layer(x: torch.Tensor, w_gate: torch.Tensor, expert_weights: torch.Tenso
               workspace: torch.Tensor | None = None, stream=None):
     """The three operators chained as the reference harness chains them (tests/test_moe.cpp:444-463).
     Returns (y, expert_ids, weights, expert_out)."""
-    ids, w = MoeRoutingTopK(x, w_gate, topK, stream)
-    eo = MoeExpertFFN(x, ids, w, expert_weights, 0, workspace, stream)
-    y = MoeCombine(eo, ids, w, topK, stream)
+    ids, w = MoeRoutingTopK(x, w_gate, topK, stream=stream)
+    eo = MoeExpertFFN(x, ids, w, expert_weights, 0, workspace, stream=stream)
+    y = MoeCombine(eo, ids, w, topK, stream=stream)
     return y, ids, w, eo
 
 

@@ -125,6 +125,23 @@ def test_plans(lib):
     assert cp.grid * cp.block * cp.elems_per_thread >= 128 * 2048 and cp.workspace_bytes == 0
 
 
+def test_ffn_plan_at_the_32bit_bounds(lib):
+    """Many rows per expert pick the LDS-tiled schedule also past 2 GiB of SwiGLU intermediate (hidden is
+    addressed per tile); past its real 32-bit bounds (2 GiB of gathered x rows) the shape is rejected, never
+    sent to the weight-streaming schedule, which would re-stream every expert's weights once per 32 rows."""
+    fp = lib_mod.FfnPlan()
+    assert lib.moe_expert_ffn_plan(65536, 2048, 16, 2, 8192, C.byref(fp)) == MOE_OK
+    assert fp.schedule == 1
+    assert fp.workspace_bytes >= 65536 * 2 * 8192 * 2  # hidden alone is 2 GiB
+    assert lib.moe_expert_ffn_plan(65536, 256, 4, 2, 8192, C.byref(fp)) == MOE_OK and fp.schedule == 1
+    # T*H*2 = 2 GiB of x: unsupported (explicitly), not the streaming schedule
+    assert lib.moe_expert_ffn_plan(1 << 20, 1024, 16, 2, 1024, C.byref(fp)) == ERR_UNSUP
+    assert b"32-bit" in lib.moe_last_error()
+    assert lib.moe_expert_ffn_workspace_bytes(1 << 20, 1024, 16, 2, 1024) == 0
+    # few rows per expert stay on the streaming schedule whatever their size
+    assert lib.moe_expert_ffn_plan(128, 2048, 16, 2, 8192, C.byref(fp)) == MOE_OK and fp.schedule == 0
+
+
 FAKE = 1 << 20  # non-null, 16-byte aligned, never dereferenced: every call below fails validation first
 
 

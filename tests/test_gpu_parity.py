@@ -407,18 +407,49 @@ def gpu_inputs(ops, cfg, seed: int):
     return x, wg, ew
 
 
-@pytest.mark.parametrize("name", ["decode", "prefill", "deepseek", "mixtral"])
+def leftover_down_rows(offsets: np.ndarray, H: int, I: int, grid: int) -> list[int]:
+    """Sorted rows, one per tile of the tiled down projection's leftover round (the tiles each XCD has left
+    after its full rounds, which the kernel splits over k into partial tiles and a fix-up): the kernel's own
+    schedule (tiles (expert, n-tile, m-tile), m fastest; XCD x owns a contiguous range, dealt round-robin to its
+    grid / 8 workgroups), restated here to choose the sample."""
+    bm, bn, xcds = 256, 256, 8
+    ntn = (H + bn - 1) // bn
+    counts = np.diff(offsets)
+    mtiles = (counts + bm - 1) // bm
+    prefix = np.concatenate([[0], np.cumsum(mtiles * ntn)])
+    total = int(prefix[-1])
+    nloc = grid // xcds
+    per_xcd = (total + xcds - 1) // xcds
+    rows = []
+    for x in range(xcds):
+        base = x * per_xcd
+        n = max(0, min(per_xcd, total - base))
+        R = n // nloc
+        for t in range(base + R * nloc, base + n):
+            e = int(np.searchsorted(prefix, t, side="right") - 1)
+            mt = (t - prefix[e]) % mtiles[e]
+            last = min(int(counts[e]), (mt + 1) * bm) - 1  # the tile's last row
+            rows.append(int(offsets[e]) + last)
+    return rows
+
+
+@pytest.mark.parametrize("name", ["small", "decode", "prefill", "deepseek", "mixtral"])
 def test_baseline_config_sampled(ops, name):
+    """Each BASELINE config at full size on the GPU generator's inputs. Routing is checked on every token;
+    expert_out and y against the oracle on a sample that holds every expert's first and last sorted row (its
+    ragged last m-tile), a row of every leftover tile of the tiled down projection (split over k), and a spread
+    of other tokens; y equals the combine of the full expert_out bit for bit on every token."""
     cfg = synth.CONFIGS[name]
     log(f"[{name}] T={cfg.T} H={cfg.H} E={cfg.E} K={cfg.K} I={cfg.I}: generating inputs on the GPU")
     x_d, wg_d, ew_d = gpu_inputs(ops, cfg, 44)
     # spot-check the device generator against numpy on slices of both weight blocks
     ew_flat = ew_d.view(-1)
     sa, sb, period, split = synth.expert_weight_sigmas(cfg)
-    for start in (0, split - 1000, period * (cfg.E - 1) + split):
-        got = host(ew_flat[start:start + 2000])
-        raw = synth.normal_f64(44, synth.STREAM_EXPERT_WEIGHTS, start, 2000)
-        sig = np.where((np.arange(start, start + 2000) % period) < split, sa, sb)
+    for start in (0, max(0, split - 1000), period * (cfg.E - 1) + split):
+        n = min(2000, ew_flat.numel() - start)
+        got = host(ew_flat[start:start + n])
+        raw = synth.normal_f64(44, synth.STREAM_EXPERT_WEIGHTS, start, n)
+        sig = np.where((np.arange(start, start + n) % period) < split, sa, sb)
         assert np.array_equal(got.view(np.uint16), (raw * sig).astype(np.float16).view(np.uint16))
 
     ids_d, w_d = ops.MoeRoutingTopK(x_d, wg_d, cfg.K)
@@ -429,19 +460,40 @@ def test_baseline_config_sampled(ops, name):
     log(f"[{name}] rows per expert: min {counts.min()} max {counts.max()}")
 
     eo_d, ws = run_ffn(ops, x_d, ids_d, w_d, ew_d, cfg.I)
-    check_permute(host(ws[: 4 * (cfg.E + 1) + 256 + 4 * cfg.slots]), ids, cfg.E)
+    ws_head = host(ws[: 4 * (cfg.E + 1) + 256 + 4 * cfg.slots])
+    check_permute(ws_head, ids, cfg.E)
     y_d = ops.MoeCombine(eo_d, ids_d, w_d, cfg.K)
     torch.cuda.synchronize()
 
-    sample = np.unique(np.linspace(0, cfg.T - 1, 6).astype(int))
-    used = np.unique(ids[sample])
+    # the sample: first and last sorted row of every expert, one row per leftover down tile, a spread of tokens
+    offsets = ws_head[: 4 * (cfg.E + 1)].view(np.int32)
+    sorted_slot = ws_head[((4 * (cfg.E + 1) + 255) // 256) * 256:][: 4 * cfg.slots].view(np.int32)
+    rows = set()
+    for e in range(cfg.E):
+        if counts[e]:
+            rows.update((int(offsets[e]), int(offsets[e + 1]) - 1))
+    leftover = []
+    if ffn_schedule(cfg.T, cfg.H, cfg.E, cfg.K, cfg.I) == 1:
+        grid = min(torch.cuda.get_device_properties(0).multi_processor_count,
+                   tiled_down_grid(cfg)) // 8 * 8
+        leftover = leftover_down_rows(offsets, cfg.H, cfg.I, grid)
+        rows.update(leftover)
+    tokens = {int(sorted_slot[r]) // cfg.K for r in rows}
+    tokens.update(np.linspace(0, cfg.T - 1, min(cfg.T, 6)).astype(int).tolist())
+    sample = np.array(sorted(tokens))
+    covered = {int(e) for e in np.unique(ids[sample])}
+    log(f"[{name}] oracle sample: {len(sample)} tokens; experts covered {len(covered)}/{int((counts > 0).sum())} "
+        f"(first and last sorted row of each); leftover down tiles covered {len(leftover)}")
+    assert covered == {e for e in range(cfg.E) if counts[e]}
+
     ew_host = np.zeros((cfg.E, 3 * cfg.I, cfg.H), np.float32)
-    for e in used:
+    for e in covered:
         ew_host[e] = f32(host(ew_d[int(e)]))
     eo_o = oracle.expert_ffn(f32(x16[sample]), ids[sample], ew_host, cfg.I)
+    del ew_host
     eo_s = f32(host(eo_d))[sample]
     m_eo = oracle.compare(eo_s, eo_o)
-    log(f"[{name}] expert_out on tokens {sample.tolist()}: {m_eo}")
+    log(f"[{name}] expert_out on {len(sample)} sampled tokens: {m_eo}")
     within(m_eo, max_abs=1e-2, mean_abs=1e-3, cos=0.9999)
     y_s = f32(host(y_d))[sample]
     y_o = oracle.combine(eo_o, f32(w[sample]))
@@ -454,6 +506,35 @@ def test_baseline_config_sampled(ops, name):
     y_chk = oracle.combine(f32(host(eo_d)), f32(w)).astype(np.float16)
     assert np.array_equal(y_all.view(np.uint16), y_chk.view(np.uint16))
     assert np.isfinite(f32(y_all)).all()
+
+
+def tiled_down_grid(cfg) -> int:
+    import ctypes as C
+
+    from conftest import package
+
+    lib_mod = package()._lib
+    plan = lib_mod.FfnPlan()
+    assert lib_mod.load().moe_expert_ffn_plan(cfg.T, cfg.H, cfg.E, cfg.K, cfg.I, C.byref(plan)) == 0
+    return plan.down_grid
+
+
+def test_reference_target_case_seed44(ops):
+    """The reference's own target-size RunTest case (tests/moe_cpu_sim.cpp:862-864: T=128, H=2048, E=16, K=2,
+    I=8192, seed 44) on its own generator's inputs rounded to fp16: ids bit-exact against the reference's
+    routing, y against its NaiveMoE output on all 128 tokens."""
+    g = load_golden("ref_target_seed44")
+    K = g["K"]
+    log("[ref seed 44] inputs regenerated and digest-checked; running the layer")
+    x_d, wg_d, ew_d = dev(g["x"]), dev(g["w_gate"]), dev(g["expert_weights"])
+    y_d, ids_d, w_d, _ = ops.moe_layer(x_d, wg_d, ew_d, K)
+    ids, w = host(ids_d), host(w_d)
+    check_routing(ids, w, g["x"], g["w_gate"], K, "ref seed 44")
+    assert np.array_equal(ids, g["expert_ids"])
+    m_y = oracle.compare(f32(host(y_d)), g["y_naive"])
+    log(f"[ref seed 44] y vs reference NaiveMoE (all tokens): {m_y}")
+    within(m_y)
+    within(m_y, max_abs=1e-2, mean_abs=1e-3, cos=0.9999)
 
 
 def ffn_schedule(T, H, E, K, I) -> int:
@@ -554,7 +635,11 @@ def test_ffn_tiled_split_leftover_round(ops):
     ids = np.stack([rng.permutation(E)[:K] for _ in range(T)]).astype(np.int32)
     w = np.full((T, K), 1.0 / K, np.float16)
     x_d, ids_d, w_d, ew_d = dev(x), dev(ids), dev(w), dev(ew)
-    eo_d, ws = run_ffn(ops, x_d, ids_d, w_d, ew_d, I)
+    with ops.kernel_trace() as launched:
+        eo_d, ws = run_ffn(ops, x_d, ids_d, w_d, ew_d, I)
+        torch.cuda.synchronize()
+    log(f"[tiled split] kernels: {sorted(launched)}")
+    assert launched.get("moe_ffn_down_fixup", (0, 0.0))[0] >= 1, "the split leftover round did not run"
     eo = host(eo_d)
     eo2_d, _ = run_ffn(ops, x_d, ids_d, w_d, ew_d, I)
     assert np.array_equal(eo.view(np.uint16), host(eo2_d).view(np.uint16)), "tiled FFN is not deterministic"
@@ -568,6 +653,60 @@ def test_ffn_tiled_split_leftover_round(ops):
     m = oracle.compare(f32(eo)[tok], eo_o)
     log(f"[tiled split T{T} H{H} E{E} K{K} I{I}] expert_out vs oracle on {len(tok)} tokens: {m}")
     within(m, max_abs=1e-2, mean_abs=1e-3, cos=0.9999)
+
+
+def test_ffn_tiled_past_2gib_hidden(ops):
+    """T*K*I*2 = 2 GiB of SwiGLU intermediate (T=65536, K=2, I=8192): the tiled kernels address hidden per tile,
+    so this shape stays on the tiled schedule. expert_out against the oracle on every expert's first and last
+    rows and a spread of tokens (H is small to keep the oracle cheap)."""
+    T, H, E, K, I = 65536, 256, 4, 2, 8192
+    assert ffn_schedule(T, H, E, K, I) == 1
+    rng = np.random.default_rng(65536)
+    x_d = torch.empty((T, H), dtype=torch.float16, device="cuda")
+    ops.synth_normal_f16_(x_d, 7, synth.STREAM_X, 1.0)
+    ew_d = torch.empty((E, 3 * I, H), dtype=torch.float16, device="cuda")
+    ops.synth_normal_f16_(ew_d, 7, synth.STREAM_EXPERT_WEIGHTS, 1.0 / math.sqrt(H), 1.0 / math.sqrt(I),
+                          3 * I * H, 2 * I * H)
+    ids = np.stack([rng.permutation(E)[:K] for _ in range(T)]).astype(np.int32)
+    w = np.full((T, K), 0.5, np.float16)
+    log(f"[2 GiB hidden] T={T} H={H} E={E} K={K} I={I}: workspace {ops.workspace_bytes(T, H, E, K, I) >> 20} MiB")
+    eo_d, ws = run_ffn(ops, x_d, dev(ids), dev(w), ew_d, I)
+    torch.cuda.synchronize()
+    check_permute(host(ws[: 4 * (E + 1) + 256 + 4 * T * K]), ids, E)
+    tok = set(np.linspace(0, T - 1, 24).astype(int).tolist())
+    for e in range(E):
+        hit = np.nonzero((ids == e).any(axis=1))[0]
+        tok.update((int(hit[0]), int(hit[-1])))
+    tok = np.array(sorted(tok))
+    eo_o = oracle.expert_ffn(f32(host(x_d[tok])), ids[tok], f32(host(ew_d)), I)
+    m = oracle.compare(f32(host(eo_d))[tok], eo_o)
+    log(f"[2 GiB hidden] expert_out vs oracle on {len(tok)} tokens: {m}")
+    within(m, max_abs=1e-2, mean_abs=1e-3, cos=0.9999)
+
+
+def test_layer_on_a_side_stream(ops):
+    """The operators queued on a stream other than torch's current one (their outputs and workspace allocated on
+    that stream): the results equal the current-stream run bit for bit, on both FFN schedules."""
+    for T, H, E, K, I in ((64, 256, 8, 2, 512), (600, 128, 8, 3, 128)):
+        gen = torch.Generator(device="cpu").manual_seed(T)
+        x = torch.randn(T, H, generator=gen).half().cuda()
+        wg = (torch.randn(H, E, generator=gen) / math.sqrt(H)).half().cuda()
+        ew = (torch.randn(E, 3 * I, H, generator=gen) / math.sqrt(H)).half().cuda()
+        ref = ops.moe_layer(x, wg, ew, K)
+        eo_f, y_f = ops.MoeExpertFFNCombine(x, ref[1], ref[2], ew)
+        torch.cuda.synchronize()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        got = ops.moe_layer(x, wg, ew, K, stream=side)
+        eo_s, y_s = ops.MoeExpertFFNCombine(x, got[1], got[2], ew, stream=side)
+        # churn the current stream's allocator while the side stream runs
+        junk = [torch.empty(1 << 20, dtype=torch.uint8, device="cuda").fill_(7) for _ in range(8)]
+        side.synchronize()
+        del junk
+        log(f"[side stream] T={T} H={H} E={E} K={K} I={I} schedule={ffn_schedule(T, H, E, K, I)}")
+        for a, b in zip(ref, got):
+            assert torch.equal(a, b)
+        assert torch.equal(eo_f, eo_s) and torch.equal(y_f, y_s)
 
 
 def test_decode_uses_streaming_and_prefill_uses_tiled():
