@@ -106,6 +106,11 @@ hipError_t launch_ffn_combine(const uint16_t* x, const int32_t* expert_ids, cons
                               const uint16_t* expert_weights, uint16_t* expert_out, uint16_t* y, FfnWorkspace ws,
                               int T, int H, int E, int K, int I, hipStream_t stream);
 
+// ---- fixed scratch of the allocation-free FFN entry point (moe_noalloc.hip) ----
+size_t noalloc_scratch_bytes();
+// the current device's scratch array, looked up once per device (hipGetSymbolAddress with that device current)
+hipError_t noalloc_scratch(void** ptr);
+
 // ---- combine (moe_combine.hip) ----
 int combine_block_threads();
 int combine_elems_per_thread();

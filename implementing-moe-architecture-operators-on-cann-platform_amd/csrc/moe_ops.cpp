@@ -259,6 +259,37 @@ moe_status moe_expert_ffn(const uint16_t* x, const int32_t* expert_ids, const ui
     return ok();
 }
 
+// MoeExpertFFN with the library's fixed per-GPU scratch as its workspace (no allocation anywhere)
+moe_status moe_expert_ffn_no_alloc(const uint16_t* x, const int32_t* expert_ids, const uint16_t* weights,
+                                   const uint16_t* expert_weights, uint16_t* expert_out, int64_t T, int64_t H,
+                                   int64_t E, int64_t K, int64_t I, void* stream) {
+    (void)weights;  // part of the operator signature; the FFN math does not use the routing weights
+    moe_status st = check_ffn_sizes(T, H, E, K, I);
+    if (st != MOE_OK) return st;
+    if (T == 0) return ok();
+    if (!x || !expert_ids || !expert_weights || !expert_out)
+        return fail(MOE_ERR_NULL, "MoeExpertFFN (no alloc): null tensor pointer");
+    if (!aligned16(x) || !aligned16(expert_weights) || !aligned16(expert_out))
+        return fail(MOE_ERR_UNSUPPORTED, "MoeExpertFFN (no alloc): x, expert_weights, expert_out must be 16-byte aligned");
+    // the tiled schedule runs its down projection unsplit here: its split partial tiles alone take up to 64 MiB
+    const size_t need = moe::ffn_workspace_bytes(T, H, E, K, I, /*tiled_split=*/false);
+    if (need > moe::noalloc_scratch_bytes())
+        return fail(MOE_ERR_UNSUPPORTED,
+                    "MoeExpertFFN (no alloc): T=%lld H=%lld E=%lld K=%lld I=%lld needs %zu bytes of workspace, the "
+                    "fixed scratch holds %zu; use moe_expert_ffn with a caller workspace",
+                    (long long)T, (long long)H, (long long)E, (long long)K, (long long)I, need,
+                    moe::noalloc_scratch_bytes());
+    void* scratch = nullptr;
+    hipError_t err = moe::noalloc_scratch(&scratch);
+    if (err != hipSuccess) return hip_fail(err, "MoeExpertFFN (no alloc): scratch address");
+    const moe::FfnWorkspace ws = moe::ffn_workspace_carve(scratch, T, H, E, K, I, /*tiled_split=*/false);
+    err = moe::launch_ffn(x, expert_ids, expert_weights, expert_out, ws, static_cast<int>(T), static_cast<int>(H),
+                          static_cast<int>(E), static_cast<int>(K), static_cast<int>(I), as_stream(stream),
+                          /*tiled_split=*/false);
+    if (err != hipSuccess) return hip_fail(err, "MoeExpertFFN (no alloc) GEMM launch");
+    return ok();
+}
+
 // MoeExpertFFN + MoeCombine in one call (optional fast path; both operators stay the contract)
 moe_status moe_expert_ffn_combine(const uint16_t* x, const int32_t* expert_ids, const uint16_t* weights,
                                   const uint16_t* expert_weights, uint16_t* expert_out, uint16_t* y,

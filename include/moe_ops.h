@@ -172,6 +172,21 @@ moe_status moe_combine_plan_for(int64_t num_tokens, int64_t hidden_size, int64_t
 moe_status moe_combine(const uint16_t* expert_out, const int32_t* expert_ids, const uint16_t* weights, uint16_t* y,
                        int64_t num_tokens, int64_t hidden_size, int64_t top_k, void* stream);
 
+/* MoeExpertFFN that allocates nothing and takes no workspace: no counterpart in the reference (whose kernel
+ * always takes a caller workspace, op_kernel/moe_expert_ffn.cpp:613-621). It is for callers that cannot
+ * allocate device memory: code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.
+ * The workspace is a fixed per-GPU device array inside the library (64 MiB, held by every GPU the library runs
+ * on until the process ends). Sizes whose workspace exceeds it return MOE_ERR_UNSUPPORTED before anything is
+ * launched (e.g. T*K*I*2 > ~60 MiB; the LDS-tiled schedule
+ * runs its down projection without the split leftover round here, so expert_out can differ from
+ * moe_expert_ffn's in fp32 summation order on that schedule; the weight-streaming schedule is bit-identical).
+ * Every call on a GPU shares that GPU's array: calls that overlap on one GPU (two streams or threads) race.
+ * Arguments, errors and outputs otherwise as moe_expert_ffn. */
+moe_status moe_expert_ffn_no_alloc(const uint16_t* x, const int32_t* expert_ids, const uint16_t* weights,
+                                   const uint16_t* expert_weights, uint16_t* expert_out, int64_t num_tokens,
+                                   int64_t hidden_size, int64_t num_experts, int64_t top_k,
+                                   int64_t intermediate_size, void* stream);
+
 /* ------------------------------------------------------------------------------------------------------
  * Optional fast path: MoeExpertFFN followed by MoeCombine in one call. It has no single counterpart in the
  * reference; it chains the kernel entries MoeExpertFFN (op_kernel/moe_expert_ffn.cpp:613-621) and MoeCombine
