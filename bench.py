@@ -23,7 +23,10 @@ Then two library kernels over 1 GiB give this box's achievable HBM rates next to
 roofline uses: a whole-line non-temporal streaming read (`hbm_read_gbps`, the access the decode weight stream
 uses) and a plain copy (`hbm_copy_gbps`, read + write); and the vendor library's dense fp16 GEMM (hipBLASLt
 through torch.matmul, 8192 x 8192 x 8192, A @ B^T) gives its achievable MFMA rate next to the published
-2.5 PFLOP/s (`gemm_fp16_tflops_library`). Kernels whose per-launch inputs fit the 256 MB Infinity
+2.5 PFLOP/s (`gemm_fp16_tflops_library`). On the decode workload a prefill pass follows (BASELINE.json
+configs[2], T=8192 with the same weights): its FFN time and MFMA fraction are `prefill_ffn_us`,
+`prefill_ffn_tflops` and `prefill_ffn_mfma_frac` (the north_star's second target), its kernels under `prefill`.
+Kernels whose per-launch inputs fit the 256 MB Infinity
 Cache (routing and combine at decode) are flagged `cache_resident`: repeated steps read them from it.
 
 The JSON line also carries:
@@ -135,6 +138,8 @@ def main() -> int:
     ap.add_argument("--cpu-target-gflop", type=float, default=30.0,
                     help="size of the CPU baseline sample in GFLOP of expert FFN work")
     ap.add_argument("--no-graph", action="store_true", help="skip the HIP-graph replay timing")
+    ap.add_argument("--no-prefill", action="store_true",
+                    help="skip the T=8192 prefill pass that the decode workload adds (prefill_* keys)")
     ap.add_argument("--no-copy-rate", action="store_true",
                     help="skip the achievable-rate probes (1 GiB read and copy, library fp16 GEMM)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -300,6 +305,56 @@ def main() -> int:
         del ga, gb, gc
         progress(f"library fp16 GEMM {n}^3: {gemm_tflops} TFLOP/s")
 
+    ffn_names = ("moe_permute", "moe_permute_scatter", "moe_ffn_gateup_swiglu", "moe_ffn_gateup_fixup", "moe_ffn_down", "moe_ffn_down_fixup",
+                 "moe_ffn_down_reduce")
+    # 8) the second north_star target on the same box: the expert FFN of the prefill workload (BASELINE.json
+    #    T=8192, same H, E, K, I, so the decode weights are reused with a new x), against the fp16 dense
+    #    MFMA peak. Routing, FFN and combine run as in the decode steps; per-kernel HIP events give the FFN time.
+    prefill = None
+    pcfg = synth.CONFIGS["prefill"]
+    if not args.no_prefill and cfg.name == "decode" and (pcfg.H, pcfg.E, pcfg.K, pcfg.I) == (H, E, K, I):
+        PT = pcfg.T
+        px = torch.empty((PT, H), dtype=torch.float16, device=dev)
+        ops.synth_normal_f16_(px, args.seed, synth.STREAM_X, 1.0)
+        pwg = torch.from_numpy(synth.gen_w_gate(pcfg, args.seed)).to(dev)
+        pids = torch.empty((PT, K), dtype=torch.int32, device=dev)
+        pw = torch.empty((PT, K), dtype=torch.float16, device=dev)
+        peo = torch.empty((PT, K, H), dtype=torch.float16, device=dev)
+        py = torch.empty((PT, H), dtype=torch.float16, device=dev)
+        pws_bytes = ops.workspace_bytes(PT, H, E, K, I)
+        pws = torch.empty(pws_bytes, dtype=torch.uint8, device=dev)
+
+        def pstep() -> None:
+            st = lib.moe_routing_topk(px.data_ptr(), pwg.data_ptr(), pids.data_ptr(), pw.data_ptr(), PT, H, E, K, sp)
+            st |= lib.moe_expert_ffn(px.data_ptr(), pids.data_ptr(), pw.data_ptr(), p["ew"], peo.data_ptr(),
+                                     pws.data_ptr(), pws_bytes, PT, H, E, K, I, sp)
+            st |= lib.moe_combine(peo.data_ptr(), pids.data_ptr(), pw.data_ptr(), py.data_ptr(), PT, H, K, sp)
+            if st:
+                raise RuntimeError(lib.moe_last_error().decode())
+
+        for _ in range(max(args.warmup, 10)):  # the shader clock ramps over the first launches of the GEMMs
+            pstep()
+        p_ms, _ = timed(pstep)
+        with ops.kernel_trace() as pk:
+            timed(pstep)
+        pavg = {n: t / c for n, (c, t) in pk.items()}
+        p_ffn_ms = sum(pavg[n] for n in ffn_names if n in pavg)
+        p_flops = 6 * PT * K * H * I
+        gu_flops = 4 * PT * K * H * I
+        prefill = {
+            "workload": f"prefill MoE layer T={PT},H={H},E={E},K={K},I={I}",
+            "layer_us": round(p_ms * 1e3, 2),
+            "ffn_us": round(p_ffn_ms * 1e3, 2),
+            "ffn_tflops": round(p_flops / (p_ffn_ms * 1e-3) / 1e12, 1),
+            "ffn_mfma_frac": round(p_flops / (p_ffn_ms * 1e-3) / 1e12 / MFMA_FP16_PEAK_TFLOPS, 4),
+            "gateup_us": round(pavg["moe_ffn_gateup_swiglu"] * 1e3, 2),
+            "gateup_mfma_frac": round(gu_flops / (pavg["moe_ffn_gateup_swiglu"] * 1e-3) / 1e12 / MFMA_FP16_PEAK_TFLOPS, 4),
+            "kernels_us": {n: round(v * 1e3, 2) for n, v in pavg.items()},
+        }
+        progress(f"prefill T={PT}: layer {prefill['layer_us']} us, FFN {prefill['ffn_us']} us = "
+                 f"{prefill['ffn_tflops']} TFLOP/s ({prefill['ffn_mfma_frac'] * 100:.1f}% of fp16 peak)")
+        del px, pwg, pids, pw, peo, py, pws
+
     ids_h = ids.cpu().numpy()
     active = int((np.bincount(ids_h.ravel(), minlength=E) > 0).sum())
     work = kernel_work(cfg, active)
@@ -312,8 +367,6 @@ def main() -> int:
                             "TFLOP/s": round(f / (avg * 1e-3) / 1e12, 2) if f else None,
                             # inputs re-read every step that fit the 256 MB Infinity Cache are served from it
                             "cache_resident": bool(b) and b < MALL_BYTES}
-    ffn_names = ("moe_permute", "moe_ffn_gateup_swiglu", "moe_ffn_gateup_fixup", "moe_ffn_down", "moe_ffn_down_fixup",
-                 "moe_ffn_down_reduce")
     ffn_ms = sum(kernels[n][1] / kernels[n][0] for n in ffn_names if n in kernels)
     ffn_flops = 6 * T * K * H * I
     ffn_bytes = active * 3 * I * H * 2 + T * H * 2 + T * K * H * 2
@@ -389,6 +442,10 @@ def main() -> int:
         "hbm_copy_gbps": copy_gbps,
         "hbm_read_gbps": read_gbps,
         "gemm_fp16_tflops_library": gemm_tflops,
+        "prefill_ffn_us": prefill["ffn_us"] if prefill else None,
+        "prefill_ffn_tflops": prefill["ffn_tflops"] if prefill else None,
+        "prefill_ffn_mfma_frac": prefill["ffn_mfma_frac"] if prefill else None,
+        "prefill": prefill,
         "roofline": roofline,
         "cpu_baseline": cpu_baseline,
         "cpu_baseline_tiled": cpu_baseline_tiled,

@@ -35,8 +35,9 @@ int ffn_schedule(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
 
 // Layout (each region 256-byte aligned): offsets [E+1] i32 | sorted_slot [T*K] i32 | hidden [T*K, I] fp16, then
 // for the weight-streaming schedule: partial [nsplit, T*K, H] fp32 (when the down projection is split over K) |
-// slot_row [T*K] i32; for the tiled schedule with tiled_split: up to 256 fp32 partial tiles of 256 x 256 (64 MiB;
-// one per workgroup of the down launch, none when I < 256) for the leftover round it splits over k.
+// slot_row [T*K] i32; for the tiled schedule: the permute's scratch (rank [T*K] i32, counts [chunks, E] i32),
+// then with tiled_split up to 256 fp32 partial tiles of 256 x 256 (64 MiB; one per workgroup of the down launch,
+// none when I < 256) for the leftover round it splits over k.
 size_t ffn_workspace_bytes(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I, bool tiled_split) {
     const size_t S = static_cast<size_t>(T) * static_cast<size_t>(K);
     size_t bytes = align_up(sizeof(int32_t) * static_cast<size_t>(E + 1), 256);
@@ -47,9 +48,11 @@ size_t ffn_workspace_bytes(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I
         bytes += align_up(stream_partial_bytes(static_cast<int>(T), static_cast<int>(H), static_cast<int>(K),
                                                static_cast<int>(I)), 256);
         bytes += align_up(sizeof(int32_t) * S, 256);
-    } else if (schedule == 1 && tiled_split) {
-        bytes += align_up(tiled_partial_bytes(static_cast<int>(T), static_cast<int>(H), static_cast<int>(E),
-                                              static_cast<int>(K), static_cast<int>(I)), 256);
+    } else if (schedule == 1) {
+        bytes += align_up(permute_scratch_bytes(static_cast<int>(S), static_cast<int>(E)), 256);
+        if (tiled_split)
+            bytes += align_up(tiled_partial_bytes(static_cast<int>(T), static_cast<int>(H), static_cast<int>(E),
+                                                  static_cast<int>(K), static_cast<int>(I)), 256);
     }
     return bytes;
 }
@@ -67,16 +70,19 @@ FfnWorkspace ffn_workspace_carve(void* base, int64_t T, int64_t H, int64_t E, in
     p += align_up(sizeof(uint16_t) * S * static_cast<size_t>(I), 256);
     ws.partial = nullptr;
     ws.slot_row = nullptr;
+    ws.pscratch = nullptr;
     const int schedule = ffn_schedule(T, H, E, K, I);
     if (schedule == 0) {
         ws.partial = reinterpret_cast<float*>(p);
         p += align_up(stream_partial_bytes(static_cast<int>(T), static_cast<int>(H), static_cast<int>(K),
                                            static_cast<int>(I)), 256);
         ws.slot_row = reinterpret_cast<int32_t*>(p);
-    } else if (schedule == 1 && tiled_split &&
-               tiled_partial_bytes(static_cast<int>(T), static_cast<int>(H), static_cast<int>(E),
-                                   static_cast<int>(K), static_cast<int>(I)) > 0) {
-        ws.partial = reinterpret_cast<float*>(p);
+    } else if (schedule == 1) {
+        ws.pscratch = reinterpret_cast<int32_t*>(p);
+        p += align_up(permute_scratch_bytes(static_cast<int>(S), static_cast<int>(E)), 256);
+        if (tiled_split && tiled_partial_bytes(static_cast<int>(T), static_cast<int>(H), static_cast<int>(E),
+                                               static_cast<int>(K), static_cast<int>(I)) > 0)
+            ws.partial = reinterpret_cast<float*>(p);
     }
     return ws;
 }

@@ -45,6 +45,7 @@ struct FfnWorkspace {
     float* partial;        // fp32 split-K partial sums: [nsplit, T*K, H] of the streaming down projection, or the
                            // tiled schedule's partial tiles of its split leftover round
     int32_t* slot_row;     // [T*K]   sorted row of each slot with a valid id (weight-streaming schedule only)
+    int32_t* pscratch;     // the permute's per-slot ranks and per-chunk counts (tiled schedule only)
 };
 // tiled_split = false leaves out the tiled schedule's partial tiles (its down projection then runs unsplit)
 size_t ffn_workspace_bytes(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I, bool tiled_split = true);
@@ -52,6 +53,8 @@ FfnWorkspace ffn_workspace_carve(void* base, int64_t T, int64_t H, int64_t E, in
                                  bool tiled_split = true);
 
 int permute_block_threads();
+int permute_chunks(int S);
+size_t permute_scratch_bytes(int S, int E);
 hipError_t prepare_permute(int S, int E);  // kernel attributes, before the first launch of a call
 hipError_t launch_permute(const int32_t* ids, int S, int E, int H, FfnWorkspace ws, uint16_t* expert_out,
                           hipStream_t stream);

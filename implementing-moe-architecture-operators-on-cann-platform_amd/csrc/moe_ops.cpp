@@ -225,7 +225,7 @@ moe_status moe_expert_ffn_plan(int64_t T, int64_t H, int64_t E, int64_t K, int64
     plan->top_k = K;
     plan->intermediate_size = I;
     plan->schedule = g.schedule;
-    plan->permute_grid = static_cast<int32_t>(E);
+    plan->permute_grid = g.schedule == 1 ? moe::permute_chunks(static_cast<int>(T * K)) : 0;
     plan->gateup_grid = g.gateup_blocks;
     plan->down_grid = g.down_blocks;
     plan->block = g.block_threads;

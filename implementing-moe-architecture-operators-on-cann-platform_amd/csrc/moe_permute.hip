@@ -4,15 +4,20 @@
 // and, for the order, the oracle's (token, slot) collection in tests/moe_cpu_sim.cpp:412-418: for each expert,
 // slots s = t*K + k in ascending order. Here there is no cap.
 //
-// One workgroup of 16 waves per expert e. The T*K ids are cut into 16 contiguous chunks, one per wave.
-//   pass 1: each wave counts, with 64-lane ballots, the ids equal to e and the valid ids below e in its chunk;
-//   the workgroup sums them: offsets[e] = #(valid ids < e), and each wave's first output row;
-//   pass 2: each wave rescans its chunk and writes the slots of expert e in ascending order.
-// Each pass is a chain of dependent round trips (16 loads per lane each). When E <= 255 and the T*K ids fit
-// the LDS as bytes, pass 1 also keeps them there and pass 2 (and the zeroing below) reads the LDS copy.
+// A stable counting sort of the T*K slots by expert id in two launches, each reading the ids once:
+//   count    one workgroup per chunk of kChunk slots. Each wave takes 256 consecutive slots, 64 at a time in slot
+//            order: lanes with the same id find each other with 8 ballots over the id's bits, so a slot's rank
+//            among the wave's earlier slots of its expert is a popcount, and one lane per expert advances the
+//            wave's running count in LDS. The chunk's per-expert counts go to counts[chunk][e] and each slot's
+//            rank within its chunk (waves before it, then its own) to rank[s].
+//   scatter  one workgroup per chunk sums column e of counts over all chunks (the expert's total) and over the
+//            chunks before this one (256 / E threads per expert); a scan over the experts gives offsets[e]; slot
+//            s of expert e goes to sorted_slot[offsets[e] + (e's slots in earlier chunks) + rank[s]]. Workgroup 0
+//            writes offsets.
 // No atomics and no cleared memory, so the result is deterministic and needs no memset before the call.
-// Slots whose id is outside [0, E) belong to no expert; the workgroups write zeros into their expert_out rows,
-// each over 1/E of the slots (one workgroup doing it alone was the kernel's critical path: 40 us at 98304 slots).
+// Slots whose id is outside [0, E) belong to no expert; the scatter workgroups write zeros into their expert_out
+// rows, each over its own chunk.
+// Replaces one workgroup per expert scanning all T*K ids (O(E*T*K) reads: 29.5 us at T*K = 98304, E = 64).
 
 #include "moe_device.h"
 #include "moe_launch.h"
@@ -21,103 +26,129 @@ namespace moe {
 
 namespace {
 
-constexpr int kPermuteWaves = 16;
-constexpr int kUnroll = 16;
-constexpr int kPermuteLdsMax = 160 * 1024 - 1024;  // byte cache of the ids (dynamic LDS), static arrays aside
+constexpr int kThreads = 256;               // 4 waves
+constexpr int kChunk = 4 * kThreads;        // slots per workgroup: 256 per wave, 64 per step
+constexpr int kMaxE = 256;                  // the library's expert limit (8 id bits)
 
-template <bool CACHE>
-__global__ __launch_bounds__(kPermuteWaves * kWave) void permute_kernel(const int32_t* __restrict__ ids, int S, int E,
-                                                                          int H, int32_t* __restrict__ offsets,
-                                                                          int32_t* __restrict__ sorted_slot,
-                                                                          uint16_t* __restrict__ expert_out) {
-    extern __shared__ uint8_t id_cache[];  // CACHE: id of slot s at [s], 255 for ids outside [0, E)
-    __shared__ int cnt_eq[kPermuteWaves];
-    __shared__ int cnt_lt[kPermuteWaves];
-    const int e = static_cast<int>(blockIdx.x);
-    const int lane = lane_id();
-    const int wave = static_cast<int>(threadIdx.x) / kWave;
-    const int chunk = (((S + kPermuteWaves - 1) / kPermuteWaves) + kWave - 1) / kWave * kWave;
-    const int beg = min(S, wave * chunk);
-    const int end = min(S, beg + chunk);
-
-    // kUnroll loads per lane are issued before their ballots: the chunk is read in a few round trips
-    int n_eq = 0, n_lt = 0;
-    for (int base = beg; base < end; base += kUnroll * kWave) {
-        int id[kUnroll];
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            const int s = base + u * kWave + lane;
-            id[u] = s < end ? ids[s] : -1;
-        }
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            const bool valid = id[u] >= 0 && id[u] < E;
-            n_eq += __popcll(__ballot(id[u] == e));
-            n_lt += __popcll(__ballot(valid && id[u] < e));
-            const int s = base + u * kWave + lane;
-            if (CACHE && s < end) id_cache[s] = static_cast<uint8_t>(valid ? id[u] : 255);
-        }
-    }
-    if (lane == 0) {
-        cnt_eq[wave] = n_eq;
-        cnt_lt[wave] = n_lt;
-    }
-    __syncthreads();  // the counts, and (CACHE) the byte copy of every chunk; each wave rereads only its own
-
-    int off = 0, before = 0, total_eq = 0;
-    for (int w = 0; w < kPermuteWaves; ++w) {
-        off += cnt_lt[w];
-        total_eq += cnt_eq[w];
-        if (w < wave) before += cnt_eq[w];
-    }
-    if (threadIdx.x == 0) {
-        offsets[e] = off;
-        if (e == E - 1) offsets[E] = off + total_eq;
-    }
-
+__global__ __launch_bounds__(kThreads) void permute_count_kernel(const int32_t* __restrict__ ids, int S, int E,
+                                                                 int32_t* __restrict__ counts,
+                                                                 int32_t* __restrict__ rank) {
+    __shared__ int wcnt[kThreads / kWave][kMaxE];  // running per-wave counts of each expert
+    const int tid = static_cast<int>(threadIdx.x);
+    const int wave = tid / kWave, lane = lane_id();
+    for (int i = tid; i < (kThreads / kWave) * kMaxE; i += kThreads) (&wcnt[0][0])[i] = 0;
+    __syncthreads();
+    const int s0 = static_cast<int>(blockIdx.x) * kChunk + wave * (kChunk / 4);
     const uint64_t below = (uint64_t{1} << lane) - 1;
-    int pos = off + before;
-    for (int base = beg; base < end; base += kUnroll * kWave) {
-        int id[kUnroll];
+    int e[4], r[4];
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            const int s = base + u * kWave + lane;
-            if (CACHE) {
-                const int c = s < end ? static_cast<int>(id_cache[s]) : 255;
-                id[u] = c == 255 ? -1 : c;
-            } else {
-                id[u] = s < end ? ids[s] : -1;
-            }
+    for (int it = 0; it < 4; ++it) {
+        const int s = s0 + it * kWave + lane;
+        e[it] = s < S ? ids[s] : -1;
+    }
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+        const bool valid = e[it] >= 0 && e[it] < E;
+        uint64_t same = __ballot(valid);  // lanes with a valid id equal to this lane's
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            const bool bit = (e[it] >> b) & 1;
+            const uint64_t m = __ballot(bit);
+            same &= bit ? m : ~m;
         }
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            const uint64_t m = __ballot(id[u] == e);
-            if (id[u] == e) sorted_slot[pos + __popcll(m & below)] = base + u * kWave + lane;
-            pos += __popcll(m);
+        const int before = __popcll(same & below);
+        r[it] = 0;
+        if (valid) {
+            r[it] = wcnt[wave][e[it]] + before;
+            // the lane of each expert's first slot advances the count; every lane's read above is issued first
+            if (before == 0) wcnt[wave][e[it]] += __popcll(same);
         }
     }
-
-    // zero the expert_out rows of ids outside [0, E): workgroup e takes slots [e * per, (e + 1) * per), read from
-    // its byte copy (CACHE) or with kUnroll loads in flight per thread
-    const int per = (S + E - 1) / E;
-    const int s_beg = min(S, e * per), s_end = min(S, s_beg + per);
-    for (int base = s_beg; base < s_end; base += kUnroll * kPermuteWaves * kWave) {
-        int id[kUnroll];
+    __syncthreads();
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            const int sl = base + u * kPermuteWaves * kWave + static_cast<int>(threadIdx.x);
-            if (CACHE) {
-                const int c = sl < s_end ? static_cast<int>(id_cache[sl]) : 0;
-                id[u] = c == 255 ? -1 : c;
-            } else {
-                id[u] = sl < s_end ? ids[sl] : 0;
+    for (int it = 0; it < 4; ++it) {
+        const int s = s0 + it * kWave + lane;
+        if (s >= S || e[it] < 0 || e[it] >= E) continue;
+        int prior = 0;  // the expert's slots in the chunk's earlier waves
+        for (int w = 0; w < wave; ++w) prior += wcnt[w][e[it]];
+        rank[s] = prior + r[it];
+    }
+    int32_t* cnt = counts + static_cast<size_t>(blockIdx.x) * E;
+    for (int x = tid; x < E; x += kThreads) {
+        int c = 0;
+#pragma unroll
+        for (int w = 0; w < kThreads / kWave; ++w) c += wcnt[w][x];
+        cnt[x] = c;
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void permute_scatter_kernel(const int32_t* __restrict__ ids, int S, int E, int H,
+                                                                   const int32_t* __restrict__ counts,
+                                                                   const int32_t* __restrict__ rank, int nchunks,
+                                                                   int32_t* __restrict__ offsets,
+                                                                   int32_t* __restrict__ sorted_slot,
+                                                                   uint16_t* __restrict__ expert_out) {
+    __shared__ int base[kMaxE];
+    __shared__ int wsum[kThreads / kWave];
+    __shared__ int part_total[kThreads], part_pre[kThreads];
+    const int tid = static_cast<int>(threadIdx.x);
+    const int wave = tid / kWave, lane = lane_id();
+    const int c = static_cast<int>(blockIdx.x);
+    // column x of counts, summed over all chunks (the expert's total) and over the chunks before c, by P = 256 / E
+    // threads per expert (thread t: expert t % E, chunks t / E, t / E + P, ...), 8 loads in flight per thread
+    const int P = kThreads / E;
+    if (tid < P * E) {
+        const int x = tid % E, part = tid / E;
+        int t_sum = 0, p_sum = 0;
+        for (int ch0 = part; ch0 < nchunks; ch0 += 8 * P) {
+            int v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int ch = ch0 + u * P;
+                v[u] = ch < nchunks ? counts[static_cast<size_t>(ch) * E + x] : 0;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                t_sum += v[u];
+                if (ch0 + u * P < c) p_sum += v[u];
             }
         }
+        part_total[tid] = t_sum;
+        part_pre[tid] = p_sum;
+    }
+    __syncthreads();
+    int total = 0, pre = 0;  // thread x < E: expert x
+    if (tid < E) {
+        for (int q = 0; q < P; ++q) {
+            total += part_total[q * E + tid];
+            pre += part_pre[q * E + tid];
+        }
+    }
+    // exclusive scan of the totals over the experts (one wave-level scan per wave, then the wave sums)
+    int incl = total;
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            if (id[u] >= 0 && id[u] < E) continue;
-            const int sl = base + u * kPermuteWaves * kWave + static_cast<int>(threadIdx.x);
-            u32x4* row = reinterpret_cast<u32x4*>(expert_out + static_cast<size_t>(sl) * H);
+    for (int d = 1; d < kWave; d <<= 1) {
+        const int v = __shfl_up(incl, d, kWave);
+        if (lane >= d) incl += v;
+    }
+    if (lane == kWave - 1) wsum[wave] = incl;
+    __syncthreads();
+    int carry = 0;
+    for (int w = 0; w < wave; ++w) carry += wsum[w];
+    const int off = carry + incl - total;
+    if (tid < E) {
+        base[tid] = off + pre;
+        if (c == 0) offsets[tid] = off;
+    }
+    if (c == 0 && tid == E - 1) offsets[E] = off + total;
+    __syncthreads();
+    const int s_end = min(S, (c + 1) * kChunk);
+    for (int s = c * kChunk + tid; s < s_end; s += kThreads) {
+        const int e = ids[s];
+        if (e >= 0 && e < E) {
+            sorted_slot[base[e] + rank[s]] = s;
+        } else {  // belongs to no expert: its expert_out row is zero
+            u32x4* row = reinterpret_cast<u32x4*>(expert_out + static_cast<size_t>(s) * H);
             for (int j = 0; j < H / 8; ++j) row[j] = u32x4{0u, 0u, 0u, 0u};
         }
     }
@@ -125,26 +156,34 @@ __global__ __launch_bounds__(kPermuteWaves * kWave) void permute_kernel(const in
 
 }  // namespace
 
-int permute_block_threads() { return kPermuteWaves * kWave; }
+int permute_block_threads() { return kThreads; }
+int permute_chunks(int S) { return (S + kChunk - 1) / kChunk; }
+
+size_t permute_scratch_bytes(int S, int E) {
+    return static_cast<size_t>(S) * sizeof(int32_t) + static_cast<size_t>(permute_chunks(S)) * E * sizeof(int32_t);
+}
 
 hipError_t prepare_permute(int S, int E) {
-    if (E <= 255 && S <= kPermuteLdsMax)
-        return ensure_lds_limit(reinterpret_cast<const void*>(&permute_kernel<true>), kPermuteLdsMax);
-    return hipSuccess;
+    (void)S;
+    (void)E;
+    return hipSuccess;  // static LDS only
 }
 
 hipError_t launch_permute(const int32_t* ids, int S, int E, int H, FfnWorkspace ws, uint16_t* expert_out,
                           hipStream_t stream) {
-    TraceScope trace("moe_permute", stream);
-    if (E <= 255 && S <= kPermuteLdsMax) {
-        const void* fn = reinterpret_cast<const void*>(&permute_kernel<true>);
-        const hipError_t attr = ensure_lds_limit(fn, kPermuteLdsMax);
-        if (attr != hipSuccess) return attr;
-        permute_kernel<true><<<E, kPermuteWaves * kWave, static_cast<size_t>(S), stream>>>(
-            ids, S, E, H, ws.offsets, ws.sorted_slot, expert_out);
-    } else {
-        permute_kernel<false><<<E, kPermuteWaves * kWave, 0, stream>>>(ids, S, E, H, ws.offsets, ws.sorted_slot,
-                                                                        expert_out);
+    const int nchunks = permute_chunks(S);
+    int32_t* rank = ws.pscratch;
+    int32_t* counts = ws.pscratch + S;
+    {
+        TraceScope trace("moe_permute", stream);
+        permute_count_kernel<<<nchunks, kThreads, 0, stream>>>(ids, S, E, counts, rank);
+    }
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    {
+        TraceScope trace("moe_permute_scatter", stream);
+        permute_scatter_kernel<<<nchunks, kThreads, 0, stream>>>(ids, S, E, H, counts, rank, nchunks, ws.offsets,
+                                                                  ws.sorted_slot, expert_out);
     }
     return hipGetLastError();
 }

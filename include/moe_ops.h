@@ -126,7 +126,9 @@ size_t moe_expert_ffn_workspace_bytes(int64_t num_tokens, int64_t hidden_size, i
 typedef struct moe_ffn_plan {
     int64_t num_tokens, hidden_size, num_experts, top_k, intermediate_size;
     int32_t schedule;        /* 0 = weight-streaming (few rows per expert), 1 = LDS-tiled (many rows)    */
-    int32_t permute_grid;    /* workgroups of the permute kernel (one per expert)                          */
+    int32_t permute_grid;    /* workgroups of each of the two permute kernels (count, scatter): one per    */
+                             /* chunk of 1024 slots; 0 on the weight-streaming schedule, whose gate/up     */
+                             /* kernel finds each expert's rows itself                                      */
     int32_t gateup_grid;     /* work tiles of the fused gate/up + SwiGLU grouped GEMM (upper bound on its */
                              /* workgroups: the streaming schedule runs a persistent grid of at most as    */
                              /* many workgroups as the GPU holds at once)                                  */

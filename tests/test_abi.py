@@ -117,7 +117,9 @@ def test_plans(lib):
     # offsets + sorted slots + the fp16 [T*K, I] intermediate + fp32 split-K partials of the down projection
     # (I = 8192 is split into 4 K-ranges of 2048) + the slot -> sorted-row map, each 256-byte aligned
     assert ws == 256 + 1024 + 128 * 2 * 8192 * 2 + 4 * 128 * 2 * 2048 * 4 + 1024
-    assert fp.permute_grid == 16 and fp.gateup_grid > 0 and fp.down_grid > 0
+    assert fp.permute_grid == 0 and fp.gateup_grid > 0 and fp.down_grid > 0  # streaming: no permute kernels
+    assert lib.moe_expert_ffn_plan(8192, 2048, 16, 2, 8192, C.byref(fp)) == MOE_OK
+    assert fp.schedule == 1 and fp.permute_grid == 16  # 16384 slots in chunks of 1024
     assert lib.moe_expert_ffn_workspace_bytes(128, 2048, 16, 2, 8200) == 0  # I % 32 != 0
     assert lib.moe_expert_ffn_plan(16384, 2048, 64, 6, 1408, C.byref(fp)) == MOE_OK
     cp = lib_mod.CombinePlan()
