@@ -7,6 +7,8 @@
 
 namespace moe {
 
+constexpr int kMaxTopK = 32;  // the largest topK the library accepts (phase 2 of routing keeps this many picks)
+
 // Per-kernel HIP-event timing (moe_trace.h). A TraceScope brackets exactly one kernel launch.
 class TraceScope {
   public:

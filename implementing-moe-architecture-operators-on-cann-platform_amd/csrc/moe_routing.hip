@@ -13,11 +13,10 @@
 //            wave's loads in one round trip), keeps partial logits of every expert block in registers and parks
 //            them in LDS.
 //   Fold:    one thread per (token, expert) adds the W partials in wave order.
-//   Phase 2: one lane per token runs softmax, top-K and renormalisation sequentially over the experts, in the
-//            oracle's order of operations: max scan from -1e30, expf(l - max), ascending-expert sum, division by
-//            the sum; K rounds of a strict '>' scan (lowest index wins an exact tie); wSum over the K picks in
-//            rank order; p / wSum; fp16 round-to-nearest-even. For E <= 64 the lane holds its row in registers
-//            (16-byte LDS reads), otherwise it works on its LDS row.
+//   Phase 2: 16 lanes per token (each holding Epad / 16 experts; four tokens per wave at a time) run the softmax,
+//            top-K and renormalisation with butterfly reductions over the group (select_group): max,
+//            expf(l - max), sum, division by the sum; K rounds of an arg-max (lowest index wins an exact tie); the
+//            renormalising sum over the K picks in rank order; fp16 round-to-nearest-even.
 // For E > 64 a wide variant runs instead: a workgroup owns 64 tokens and each of its 4 waves 16 of them over
 // all of H, so no partials are folded. w_gate reaches the waves through LDS: 32-row chunks are read with
 // coalesced loads (one row of E experts is contiguous) and written transposed, [expert][h], so a lane's
@@ -36,6 +35,7 @@ namespace moe {
 namespace {
 
 constexpr int kTokensPerBlock = 16;
+constexpr int kSelLanes = 16;  // lanes that select one token's experts (phase 2)
 
 // The narrow kernel runs E <= 64. The wave count fixes each token's summation order (wave w adds the k-steps
 // w, w + W, ... and the partials are folded in wave order), so it does not depend on the token blocks: a token's
@@ -54,75 +54,87 @@ constexpr size_t narrow_lds_bytes(int eb, int tb) {
     return static_cast<size_t>(waves_for(eb, tb)) * 16 * tb * eb * 16 * sizeof(float);
 }
 
-// softmax + top-K + renormalisation of one token's logits L[0..E) held in registers (Epad = EB * 16 >= E)
-template <int Epad>
-__device__ __forceinline__ void select_registers(float (&L)[Epad], float* picked, int E, int K, int32_t* ids_out,
-                                                 uint16_t* w_out) {
-    float mx = -1e30f;
+// Softmax, top-K and renormalisation of one token per group of G lanes (a power of two, groups aligned in the
+// wave); group lane gl holds experts gl + G q, q < EPL, of the token's logits row (fp32, in LDS). Every
+// reduction is a butterfly over the group (xor shuffles): the max and the arg-max (lowest index wins an exact
+// tie, as the reference's strict '>' scans) are exact in any order; the softmax sum adds in a fixed association,
+// identical in every lane of the group, so a token's result does not depend on its batch. Probabilities are
+// exp(l - max) / sum, the K picks come in descending order, and their renormalisation sums them in rank order
+// (the oracle's order, tests/moe_cpu_sim.cpp:224-243); lane gl writes picks gl, gl + G, ... below K. Padding experts (e >= E) and
+// picked experts hold -2, below every probability. All lanes of the wave must call this (shuffles); only groups
+// with `active` set write.
+template <int G, int EPL>
+__device__ __forceinline__ void select_group(const float* row, int E, int K, bool active, int32_t* ids_out,
+                                             uint16_t* w_out) {
+    const int gl = lane_id() & (G - 1);
+    float v[EPL];
+    float mx = -1e30f;  // the oracle's starting maximum
 #pragma unroll
-    for (int e = 0; e < Epad; ++e)
-        if (e < E && L[e] > mx) mx = L[e];
-    float total = 0.0f;
-#pragma unroll
-    for (int e = 0; e < Epad; ++e) {
-        if (e < E) {
-            L[e] = expf(L[e] - mx);
-            total += L[e];
-        }
+    for (int q = 0; q < EPL; ++q) {
+        const int e = gl + G * q;
+        v[q] = e < E ? row[e] : -1e30f;
+        mx = fmaxf(mx, v[q]);
     }
 #pragma unroll
-    for (int e = 0; e < Epad; ++e) L[e] = e < E ? L[e] / total : -2.0f;  // padding never wins a pick
-    float sel = 0.0f;
-    for (int k = 0; k < K; ++k) {
-        float best = -1.0f;
-        int bi = 0;
+    for (int d = 1; d < G; d <<= 1) mx = fmaxf(mx, __shfl_xor(mx, d, kWave));
+    float total = 0.0f;
 #pragma unroll
-        for (int e = 0; e < Epad; ++e) {
-            if (L[e] > best) {
-                best = L[e];
-                bi = e;
+    for (int q = 0; q < EPL; ++q) {
+        v[q] = gl + G * q < E ? expf(v[q] - mx) : 0.0f;
+        total += v[q];
+    }
+#pragma unroll
+    for (int d = 1; d < G; d <<= 1) total += __shfl_xor(total, d, kWave);
+#pragma unroll
+    for (int q = 0; q < EPL; ++q) v[q] = gl + G * q < E ? v[q] / total : -2.0f;
+    constexpr int NP = (kMaxTopK + G - 1) / G;  // picks a lane keeps: pick k sits in lane k % G, slot k / G
+    float sel = 0.0f, my_p[NP];
+    int my_id[NP];
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+        my_p[j] = 0.0f;
+        my_id[j] = 0;
+    }
+    for (int k = 0; k < K; ++k) {
+        float bv = -3.0f;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int q = 0; q < EPL; ++q) {  // q ascending: within a lane the lower index keeps an exact tie
+            if (v[q] > bv) {
+                bv = v[q];
+                bi = gl + G * q;
             }
         }
 #pragma unroll
-        for (int e = 0; e < Epad; ++e)
-            if (e == bi) L[e] = -2.0f;  // probabilities are >= 0, so a picked expert never wins again
-        ids_out[k] = bi;
-        picked[k] = best;
-        sel += best;
-    }
-    for (int k = 0; k < K; ++k) w_out[k] = f32_to_f16_bits(picked[k] / sel);
-}
-
-// the same on the token's LDS row (any E)
-__device__ __forceinline__ void select_lds(float* L, float* picked, int E, int K, int32_t* ids_out,
-                                           uint16_t* w_out) {
-    float mx = -1e30f;
-    for (int e = 0; e < E; ++e)
-        if (L[e] > mx) mx = L[e];
-    float total = 0.0f;
-    for (int e = 0; e < E; ++e) {
-        const float p = expf(L[e] - mx);
-        L[e] = p;
-        total += p;
-    }
-    for (int e = 0; e < E; ++e) L[e] = L[e] / total;
-    float sel = 0.0f;
-    for (int k = 0; k < K; ++k) {
-        float best = -1.0f;
-        int bi = 0;
-        for (int e = 0; e < E; ++e) {
-            const float v = L[e];
-            if (v > best) {
-                best = v;
-                bi = e;
+        for (int d = 1; d < G; d <<= 1) {
+            const float ov = __shfl_xor(bv, d, kWave);
+            const int oi = __shfl_xor(bi, d, kWave);
+            if (ov > bv || (ov == bv && oi < bi)) {
+                bv = ov;
+                bi = oi;
             }
         }
-        ids_out[k] = bi;
-        picked[k] = best;
-        sel += best;
-        L[bi] = -2.0f;
+#pragma unroll
+        for (int q = 0; q < EPL; ++q)
+            if (gl + G * q == bi) v[q] = -2.0f;  // probabilities are >= 0: a picked expert never wins again
+#pragma unroll
+        for (int j = 0; j < NP; ++j) {
+            if (k == gl + G * j) {
+                my_id[j] = bi;
+                my_p[j] = bv;
+            }
+        }
+        sel += bv;
     }
-    for (int k = 0; k < K; ++k) w_out[k] = f32_to_f16_bits(picked[k] / sel);
+    if (active) {
+#pragma unroll
+        for (int j = 0; j < NP; ++j) {
+            if (gl + G * j < K) {
+                ids_out[gl + G * j] = my_id[j];
+                w_out[gl + G * j] = f32_to_f16_bits(my_p[j] / sel);
+            }
+        }
+    }
 }
 
 // EB = number of 16-expert blocks held in registers (ceil(E / 16) rounded up to an instantiated size); TB = 16-token
@@ -209,23 +221,14 @@ __global__ __launch_bounds__(waves_for(EB, TB) * kWave) void routing_topk_kernel
     }
     __syncthreads();
 
-    // ---- phase 2: one lane per token ----
-    if (threadIdx.x >= NT) return;
-    const int t = static_cast<int>(threadIdx.x);
-    if (t0 + t >= T) return;
-    int32_t* ids_out = expert_ids + static_cast<size_t>(t0 + t) * K;
-    uint16_t* w_out = weights + static_cast<size_t>(t0 + t) * K;
-    if constexpr (EB <= 4) {
-        float L[Epad];
-#pragma unroll
-        for (int e = 0; e < Epad; e += 4) {
-            const f32x4 v = *reinterpret_cast<const f32x4*>(part + t * Epad + e);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) L[e + j] = v[j];
-        }
-        select_registers<Epad>(L, part + (NT + t) * Epad, E, K, ids_out, w_out);  // K <= E <= Epad
-    } else {
-        select_lds(part + t * Epad, part + (NT + t) * Epad, E, K, ids_out, w_out);  // wave-1 rows are free now
+    // ---- phase 2: 16 lanes per token (EB experts a lane), 4 tokens per wave at a time ----
+    constexpr int TPW = kWave / kSelLanes;  // tokens per wave and round
+    for (int tb = wave * TPW; tb < NT; tb += W * TPW) {
+        const int t = tb + lane / kSelLanes;
+        const bool active = t < NT && t0 + t < T;
+        const int tr = min(t, NT - 1);  // inactive groups read a valid row and write nothing
+        select_group<kSelLanes, EB>(part + tr * Epad, E, K, active, expert_ids + static_cast<size_t>(t0 + tr) * K,
+                                    weights + static_cast<size_t>(t0 + tr) * K);
     }
 }
 
@@ -330,23 +333,14 @@ __global__ __launch_bounds__(kWideWaves * kWave) void routing_wide_kernel(const 
         for (int r = 0; r < 4; ++r) logits[(wave * 16 + kg * 4 + r) * Epad + b * 16 + row] = acc[b][r];
     __syncthreads();
 
-    // ---- one lane per token (wave 0) ----
-    if (tid >= kWideTokens || t0 + tid >= T) return;
-    const int t = tid;
-    int32_t* ids_out = expert_ids + static_cast<size_t>(t0 + t) * K;
-    uint16_t* w_out = weights + static_cast<size_t>(t0 + t) * K;
-    float* picked = reinterpret_cast<float*>(wt) + t * 32;  // the w_gate buffers are free now: 32 floats a token
-    if constexpr (EB <= 4) {
-        float L[Epad];
-#pragma unroll
-        for (int e = 0; e < Epad; e += 4) {
-            const f32x4 v = *reinterpret_cast<const f32x4*>(logits + t * Epad + e);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) L[e + j] = v[j];
-        }
-        select_registers<Epad>(L, picked, E, K, ids_out, w_out);
-    } else {
-        select_lds(logits + t * Epad, picked, E, K, ids_out, w_out);
+    // ---- 16 lanes per token (EB experts a lane), 4 tokens per wave at a time ----
+    constexpr int TPW = kWave / kSelLanes;
+    for (int tb = wave * TPW; tb < kWideTokens; tb += kWideWaves * TPW) {
+        const int t = tb + lane / kSelLanes;
+        const bool active = t0 + t < T;
+        select_group<kSelLanes, EB>(logits + t * Epad, E, K, active,
+                                    expert_ids + static_cast<size_t>(active ? t0 + t : 0) * K,
+                                    weights + static_cast<size_t>(active ? t0 + t : 0) * K);
     }
 }
 
