@@ -13,8 +13,8 @@
 //            wave's loads in one round trip), keeps partial logits of every expert block in registers and parks
 //            them in LDS.
 //   Fold:    one thread per (token, expert) adds the W partials in wave order.
-//   Phase 2: 16 lanes per token (each holding Epad / 16 experts; four tokens per wave at a time) run the softmax,
-//            top-K and renormalisation with butterfly reductions over the group (select_group): max,
+//   Phase 2: one 16-lane DPP row per token (each lane holding Epad / 16 experts; four tokens per wave at a time)
+//            runs the softmax, top-K and renormalisation with all-reduces over the row (select_row): max,
 //            expf(l - max), sum, division by the sum; K rounds of an arg-max (lowest index wins an exact tie); the
 //            renormalising sum over the K picks in rank order; fp16 round-to-nearest-even.
 // For E > 64 a wide variant runs instead: a workgroup owns 64 tokens and each of its 4 waves 16 of them over
@@ -35,7 +35,7 @@ namespace moe {
 namespace {
 
 constexpr int kTokensPerBlock = 16;
-constexpr int kSelLanes = 16;  // lanes that select one token's experts (phase 2)
+constexpr int kSelLanes = 16;  // lanes that select one token's experts (phase 2): one DPP row
 
 // The narrow kernel runs E <= 64. The wave count fixes each token's summation order (wave w adds the k-steps
 // w, w + W, ... and the partials are folded in wave order), so it does not depend on the token blocks: a token's
@@ -50,22 +50,50 @@ constexpr int unroll_for(int eb, int tb) {
 // 16-token blocks per workgroup of the narrow kernel: each w_gate fragment a wave loads feeds tb of them. As many
 // as keep the grid at >= 256 workgroups (one per CU).
 int narrow_token_blocks(int T) { return T >= 16 * 4 * 256 ? 4 : T >= 16 * 2 * 256 ? 2 : 1; }
-constexpr size_t narrow_lds_bytes(int eb, int tb) {
-    return static_cast<size_t>(waves_for(eb, tb)) * 16 * tb * eb * 16 * sizeof(float);
+// partial logits, then (lw) every wave's U w_gate stages of 32 rows
+constexpr size_t narrow_lds_bytes(int eb, int tb, bool lw) {
+    return static_cast<size_t>(waves_for(eb, tb)) * 16 * eb *
+           (tb * 16 * sizeof(float) + (lw ? unroll_for(eb, tb) * 32 * sizeof(uint16_t) : 0));
+}
+// the LDS path for w_gate: whole 16-byte chunks per row, an aligned base, 32-bit buffer offsets
+bool narrow_lds_weights(const void* w_gate, int H, int E) {
+    return E % 8 == 0 && (reinterpret_cast<uintptr_t>(w_gate) & 15) == 0 &&
+           static_cast<int64_t>(H) * E * 2 < (int64_t{1} << 31);
 }
 
-// Softmax, top-K and renormalisation of one token per group of G lanes (a power of two, groups aligned in the
-// wave); group lane gl holds experts gl + G q, q < EPL, of the token's logits row (fp32, in LDS). Every
-// reduction is a butterfly over the group (xor shuffles): the max and the arg-max (lowest index wins an exact
-// tie, as the reference's strict '>' scans) are exact in any order; the softmax sum adds in a fixed association,
-// identical in every lane of the group, so a token's result does not depend on its batch. Probabilities are
-// exp(l - max) / sum, the K picks come in descending order, and their renormalisation sums them in rank order
-// (the oracle's order, tests/moe_cpu_sim.cpp:224-243); lane gl writes picks gl, gl + G, ... below K. Padding experts (e >= E) and
-// picked experts hold -2, below every probability. All lanes of the wave must call this (shuffles); only groups
-// with `active` set write.
-template <int G, int EPL>
-__device__ __forceinline__ void select_group(const float* row, int E, int K, bool active, int32_t* ids_out,
-                                             uint16_t* w_out) {
+// Keeps the larger of two (probability, expert) candidates; an exact tie goes to the lower expert index.
+__device__ __forceinline__ void argmax_step(float& bv, int& bi, float ov, int oi) {
+    const bool take = (ov > bv) | ((ov == bv) & (oi < bi));  // no short circuit: two selects, no branch
+    bv = take ? ov : bv;
+    bi = take ? oi : bi;
+}
+
+// The 16-lane all-reduce runs on DPP row operations (a VALU operand modifier, no LDS round trip). Step 0 pairs
+// lane i with i ^ 1 and step 1 with i ^ 2 (quad permutes); step 2 mirrors each half row (i <-> 7 - i, which
+// pairs the two quads of the half, each already uniform) and step 3 the row (i <-> 15 - i, pairing the halves).
+// Every lane ends with the row's result and the association is the same as a xor-1/2/4/8 butterfly's.
+template <int STEP>
+__device__ __forceinline__ int row_partner(int v) {
+    constexpr int ctrl = STEP == 0 ? 0xB1 : STEP == 1 ? 0x4E : STEP == 2 ? 0x141 : 0x140;
+    return __builtin_amdgcn_mov_dpp(v, ctrl, 0xF, 0xF, false);
+}
+template <int STEP>
+__device__ __forceinline__ float row_partner(float v) {
+    return __builtin_bit_cast(float, row_partner<STEP>(__builtin_bit_cast(int, v)));
+}
+
+// Softmax, top-K and renormalisation of one token per 16-lane DPP row (four tokens per wave); row lane gl holds
+// experts gl + 16 q, q < EPL, of the token's logits row (fp32, in LDS). The max and the arg-max (lowest index
+// wins an exact tie, as the reference's strict '>' scans) are exact in any order; the softmax sum adds in one
+// fixed association, identical in every lane of the row, so a token's result does not depend on its batch.
+// Probabilities are exp(l - max) / sum, the K picks come in descending order, and their renormalisation sums
+// them in rank order (the oracle's order, tests/moe_cpu_sim.cpp:224-243); lane gl writes picks gl, gl + 16, ...
+// below K. Padding experts (e >= E) and picked experts hold -2, below every probability. All 64 lanes of the
+// wave must call this (DPP reads the neighbours' registers); only rows with `active` set write.
+template <int EPL>
+__device__ __forceinline__ void select_row(const float* row, int E, int K, bool active, int32_t* ids_out,
+                                           uint16_t* w_out) {
+    constexpr int G = kSelLanes;
     const int gl = lane_id() & (G - 1);
     float v[EPL];
     float mx = -1e30f;  // the oracle's starting maximum
@@ -75,19 +103,23 @@ __device__ __forceinline__ void select_group(const float* row, int E, int K, boo
         v[q] = e < E ? row[e] : -1e30f;
         mx = fmaxf(mx, v[q]);
     }
-#pragma unroll
-    for (int d = 1; d < G; d <<= 1) mx = fmaxf(mx, __shfl_xor(mx, d, kWave));
+    mx = fmaxf(mx, row_partner<0>(mx));
+    mx = fmaxf(mx, row_partner<1>(mx));
+    mx = fmaxf(mx, row_partner<2>(mx));
+    mx = fmaxf(mx, row_partner<3>(mx));
     float total = 0.0f;
 #pragma unroll
     for (int q = 0; q < EPL; ++q) {
         v[q] = gl + G * q < E ? expf(v[q] - mx) : 0.0f;
         total += v[q];
     }
-#pragma unroll
-    for (int d = 1; d < G; d <<= 1) total += __shfl_xor(total, d, kWave);
+    total += row_partner<0>(total);
+    total += row_partner<1>(total);
+    total += row_partner<2>(total);
+    total += row_partner<3>(total);
 #pragma unroll
     for (int q = 0; q < EPL; ++q) v[q] = gl + G * q < E ? v[q] / total : -2.0f;
-    constexpr int NP = (kMaxTopK + G - 1) / G;  // picks a lane keeps: pick k sits in lane k % G, slot k / G
+    constexpr int NP = EPL;  // K <= E <= 16 EPL picks; pick k sits in lane k % 16, slot k / 16
     float sel = 0.0f, my_p[NP];
     int my_id[NP];
 #pragma unroll
@@ -105,21 +137,16 @@ __device__ __forceinline__ void select_group(const float* row, int E, int K, boo
                 bi = gl + G * q;
             }
         }
-#pragma unroll
-        for (int d = 1; d < G; d <<= 1) {
-            const float ov = __shfl_xor(bv, d, kWave);
-            const int oi = __shfl_xor(bi, d, kWave);
-            if (ov > bv || (ov == bv && oi < bi)) {
-                bv = ov;
-                bi = oi;
-            }
-        }
+        argmax_step(bv, bi, row_partner<0>(bv), row_partner<0>(bi));
+        argmax_step(bv, bi, row_partner<1>(bv), row_partner<1>(bi));
+        argmax_step(bv, bi, row_partner<2>(bv), row_partner<2>(bi));
+        argmax_step(bv, bi, row_partner<3>(bv), row_partner<3>(bi));
 #pragma unroll
         for (int q = 0; q < EPL; ++q)
             if (gl + G * q == bi) v[q] = -2.0f;  // probabilities are >= 0: a picked expert never wins again
 #pragma unroll
         for (int j = 0; j < NP; ++j) {
-            if (k == gl + G * j) {
+            if ((k >> 4) == j && (k & (G - 1)) == gl) {  // the first test is uniform over the wave
                 my_id[j] = bi;
                 my_p[j] = bv;
             }
@@ -137,9 +164,27 @@ __device__ __forceinline__ void select_group(const float* row, int E, int K, boo
     }
 }
 
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16 (gfx950): 8 bytes per lane, handed out transposed within each 16-lane group
+__device__ __forceinline__ s16x4 lds_read_tr16(const uint8_t* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(p));
+}
+
+// LDS byte offset, inside a wave's w_gate stage ([32 rows][Epad] fp16, rows of 2 Epad 16-byte chunks), of the
+// 16-byte chunk c of row r: chunks are XOR-swizzled by the row so that the transposing reads spread over the banks.
+template <int EB>
+__device__ __forceinline__ int wstage_chunk(int r, int c) {
+    return (r * 2 * EB + (c ^ (r & (2 * EB - 1)))) * 16;
+}
+
 // EB = number of 16-expert blocks held in registers (ceil(E / 16) rounded up to an instantiated size); TB = 16-token
-// blocks per workgroup (every w_gate fragment a wave loads is multiplied into all TB of them).
-template <int EB, int TB>
+// blocks per workgroup (every w_gate fragment a wave loads is multiplied into all TB of them). LW: w_gate rows
+// reach the wave through LDS (E % 8 == 0 and a 16-byte aligned w_gate): each k-step's 32 rows are copied with
+// 16-byte direct-to-LDS loads in their own row-major layout and the B fragments (8 consecutive h of one expert)
+// come out of ds_read_tr16_b64, which hands lane i of each 16-lane group element i % 4 of the 4-element rows
+// addressed by lanes 4 j + i / 4 (j < 4). Without LW every fragment is 8 strided 2-byte global loads.
+template <int EB, int TB, bool LW>
 __global__ __launch_bounds__(waves_for(EB, TB) * kWave) void routing_topk_kernel(const uint16_t* __restrict__ x,
                                                                               const uint16_t* __restrict__ w_gate,
                                                                               int32_t* __restrict__ expert_ids,
@@ -149,9 +194,10 @@ __global__ __launch_bounds__(waves_for(EB, TB) * kWave) void routing_topk_kernel
     constexpr int U = unroll_for(EB, TB);
     constexpr int Epad = EB * 16;
     constexpr int NT = 16 * TB;  // tokens per workgroup
-    extern __shared__ float part[];  // [W][NT tokens][Epad] fp32 partial logits; row (0, t) receives the fold
+    // [W][NT tokens][Epad] fp32 partial logits (row (0, t) receives the fold); with LW then [W][U][32][Epad] fp16
+    extern __shared__ float part[];
     const int lane = lane_id();
-    const int wave = static_cast<int>(threadIdx.x) / kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);  // uniform: scalar loops
     const int row = lane & 15;  // A row (token) / B column (expert) owned by this lane
     const int kg = lane >> 4;   // k-group: 8 consecutive k of each 32-wide k-step
     const int t0 = static_cast<int>(blockIdx.x) * NT;
@@ -170,6 +216,30 @@ __global__ __launch_bounds__(waves_for(EB, TB) * kWave) void routing_topk_kernel
         for (int b = 0; b < EB; ++b) acc[tb][b] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     const int nsteps = H / 32;
+    // LW: this wave's U stages, the buffer resource over w_gate, and each lane's copy and fragment offsets
+    uint8_t* wst = reinterpret_cast<uint8_t*>(part + W * NT * Epad) + wave * (U * 32 * Epad * 2);
+    const __amdgpu_buffer_rsrc_t wrs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(w_gate), 0, LW ? H * E * 2 : 0, 0x00020000);
+    int cpy_off[EB];     // byte offset in w_gate (relative to the k-step's first row) of the chunk this lane copies
+    int frag_off[2][EB]; // byte offset in a stage of the 8 bytes this lane addresses for half h of expert block b
+    if constexpr (LW) {
+#pragma unroll
+        for (int i = 0; i < EB; ++i) {  // copy i fills stage bytes [1024 i, 1024 i + 1024): lane -> 16-byte slot
+            const int slot = i * kWave + lane;
+            const int r = slot / (2 * EB), pc = slot % (2 * EB);
+            const int c = pc ^ (r & (2 * EB - 1));     // the logical chunk that belongs in physical slot pc
+            cpy_off[i] = (r * E + (c * 8 < E ? c * 8 : 0)) * 2;  // padding chunks copy any valid chunk
+        }
+        const int g = lane >> 4, sl = lane & 15;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int b = 0; b < EB; ++b) {
+                const int r = 8 * g + 4 * h + sl / 4;
+                const int e = 16 * b + 4 * (sl % 4);
+                frag_off[h][b] = wstage_chunk<EB>(r, e / 8) + (e % 8) * 2;
+            }
+    }
     for (int s0 = wave; s0 < nsteps; s0 += U * W) {
         f16x8 a[U][TB];
         f16x8 bv[U][EB];
@@ -186,14 +256,42 @@ __global__ __launch_bounds__(waves_for(EB, TB) * kWave) void routing_topk_kernel
                     for (int q = 0; q < 8; ++q) a[u][tb][q] = static_cast<f16>(0.0f);
                 }
             }
-            const uint16_t* wrow = w_gate + static_cast<size_t>(k0 + kg * 8) * E;
+            if constexpr (LW) {
+                if (in) {
 #pragma unroll
-            for (int b = 0; b < EB; ++b) {
-                const int e = b * 16 + row;
+                    for (int i = 0; i < EB; ++i)
+                        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                            wrs, (__attribute__((address_space(3))) void*)(wst + (u * 32 * Epad * 2) + i * 1024), 16,
+                            static_cast<int>(cpy_off[i]), k0 * E * 2, 0, 0);  // (the cast keeps the host pass's launch stub)
+                }
+            } else {
+                const uint16_t* wrow = w_gate + static_cast<size_t>(k0 + kg * 8) * E;
 #pragma unroll
-                for (int q = 0; q < 8; ++q)
-                    bv[u][b][q] = (in && e < E) ? __builtin_bit_cast(f16, wrow[static_cast<size_t>(q) * E + e])
-                                                : static_cast<f16>(0.0f);
+                for (int b = 0; b < EB; ++b) {
+                    const int e = b * 16 + row;
+#pragma unroll
+                    for (int q = 0; q < 8; ++q)
+                        bv[u][b][q] = (in && e < E) ? __builtin_bit_cast(f16, wrow[static_cast<size_t>(q) * E + e])
+                                                    : static_cast<f16>(0.0f);
+                }
+            }
+        }
+        if constexpr (LW) {
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // this wave's stage copies have landed in LDS
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const bool in = s0 + u * W < nsteps;
+#pragma unroll
+                for (int b = 0; b < EB; ++b) {
+                    if (in) {
+                        const uint8_t* st = wst + u * 32 * Epad * 2;
+                        const s16x4 lo = lds_read_tr16(st + frag_off[0][b]);
+                        const s16x4 hi = lds_read_tr16(st + frag_off[1][b]);
+                        bv[u][b] = __builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+                    } else {
+                        bv[u][b] = f16x8{};
+                    }
+                }
             }
         }
 #pragma unroll
@@ -213,11 +311,12 @@ __global__ __launch_bounds__(waves_for(EB, TB) * kWave) void routing_topk_kernel
     __syncthreads();
 
     // ---- fold: partial of wave 0 + wave 1 + ... in wave order, into the wave-0 rows ----
-    for (int i = static_cast<int>(threadIdx.x); i < NT * Epad; i += W * kWave) {
-        float v = part[i];
+    f32x4* part4 = reinterpret_cast<f32x4*>(part);
+    for (int i = static_cast<int>(threadIdx.x); i < NT * Epad / 4; i += W * kWave) {
+        f32x4 v = part4[i];
 #pragma unroll
-        for (int w = 1; w < W; ++w) v += part[w * NT * Epad + i];
-        part[i] = v;
+        for (int w = 1; w < W; ++w) v += part4[w * NT * Epad / 4 + i];
+        part4[i] = v;
     }
     __syncthreads();
 
@@ -227,7 +326,7 @@ __global__ __launch_bounds__(waves_for(EB, TB) * kWave) void routing_topk_kernel
         const int t = tb + lane / kSelLanes;
         const bool active = t < NT && t0 + t < T;
         const int tr = min(t, NT - 1);  // inactive groups read a valid row and write nothing
-        select_group<kSelLanes, EB>(part + tr * Epad, E, K, active, expert_ids + static_cast<size_t>(t0 + tr) * K,
+        select_row<EB>(part + tr * Epad, E, K, active, expert_ids + static_cast<size_t>(t0 + tr) * K,
                                     weights + static_cast<size_t>(t0 + tr) * K);
     }
 }
@@ -255,7 +354,7 @@ __global__ __launch_bounds__(kWideWaves * kWave) void routing_wide_kernel(const 
     float* logits = reinterpret_cast<float*>(wt + 2 * Epad * P);     // [64 tokens][Epad] fp32
     const int tid = static_cast<int>(threadIdx.x);
     const int lane = lane_id();
-    const int wave = tid / kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int row = lane & 15, kg = lane >> 4;
     const int t0 = static_cast<int>(blockIdx.x) * kWideTokens;
     const int tok = min(t0 + wave * 16 + row, T - 1);  // rows past T read a valid row; results are dropped
@@ -338,7 +437,7 @@ __global__ __launch_bounds__(kWideWaves * kWave) void routing_wide_kernel(const 
     for (int tb = wave * TPW; tb < kWideTokens; tb += kWideWaves * TPW) {
         const int t = tb + lane / kSelLanes;
         const bool active = t0 + t < T;
-        select_group<kSelLanes, EB>(logits + t * Epad, E, K, active,
+        select_row<EB>(logits + t * Epad, E, K, active,
                                     expert_ids + static_cast<size_t>(active ? t0 + t : 0) * K,
                                     weights + static_cast<size_t>(active ? t0 + t : 0) * K);
     }
@@ -363,17 +462,24 @@ hipError_t launch_wide(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, 
     return hipGetLastError();
 }
 
-template <int EB, int TB>
+template <int EB, int TB, bool LW>
 hipError_t launch_narrow(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H, int E,
                          int K, hipStream_t stream) {
     const int grid = (T + 16 * TB - 1) / (16 * TB);
-    const size_t lds = narrow_lds_bytes(EB, TB);
-    const hipError_t attr = ensure_lds_limit(reinterpret_cast<const void*>(&routing_topk_kernel<EB, TB>),
+    const size_t lds = narrow_lds_bytes(EB, TB, LW);
+    const hipError_t attr = ensure_lds_limit(reinterpret_cast<const void*>(&routing_topk_kernel<EB, TB, LW>),
                                              static_cast<int>(lds));
     if (attr != hipSuccess) return attr;
     TraceScope trace("moe_routing_topk", stream);
-    routing_topk_kernel<EB, TB><<<grid, waves_for(EB, TB) * kWave, lds, stream>>>(x, w_gate, ids, w, T, H, E, K);
+    routing_topk_kernel<EB, TB, LW><<<grid, waves_for(EB, TB) * kWave, lds, stream>>>(x, w_gate, ids, w, T, H, E, K);
     return hipGetLastError();
+}
+
+template <int EB, int TB>
+hipError_t launch_narrow(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H, int E,
+                         int K, hipStream_t stream) {
+    return narrow_lds_weights(w_gate, H, E) ? launch_narrow<EB, TB, true>(x, w_gate, ids, w, T, H, E, K, stream)
+                                            : launch_narrow<EB, TB, false>(x, w_gate, ids, w, T, H, E, K, stream);
 }
 
 template <int EB>
@@ -407,7 +513,7 @@ int routing_block_threads(int T, int E) {
 int routing_lds_bytes(int T, int E) {
     const int eb = routing_expert_blocks(E);
     if (eb > 4) return static_cast<int>(wide_lds_bytes(eb));
-    return static_cast<int>(narrow_lds_bytes(eb, narrow_token_blocks(T)));
+    return static_cast<int>(narrow_lds_bytes(eb, narrow_token_blocks(T), E % 8 == 0));
 }
 
 hipError_t launch_routing_topk(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H,
