@@ -48,8 +48,13 @@ constexpr int unroll_for(int eb, int tb) {
     return tb == 1 ? (eb == 1 ? 4 : eb == 2 ? 2 : 4) : eb == 1 ? (tb == 2 ? 4 : 2) : eb == 2 ? (tb == 2 ? 2 : 1) : 2;
 }
 // 16-token blocks per workgroup of the narrow kernel: each w_gate fragment a wave loads feeds tb of them. As many
-// as keep the grid at >= 256 workgroups (one per CU).
-int narrow_token_blocks(int T) { return T >= 16 * 4 * 256 ? 4 : T >= 16 * 2 * 256 ? 2 : 1; }
+// as keep the grid at >= 256 workgroups (one per CU), but at most 2 for 32 < E <= 64: two workgroups of 64 KB
+// LDS then share a CU and one's selection phase overlaps the other's loads (T = 16384, E = 64: 22.8 us against
+// 25.9 us with 4 blocks, 25.8 us with 1).
+int narrow_token_blocks(int T, int eb) {
+    const int tb = T >= 16 * 4 * 256 ? 4 : T >= 16 * 2 * 256 ? 2 : 1;
+    return eb == 4 ? min(tb, 2) : tb;
+}
 // partial logits, then (lw) every wave's U w_gate stages of 32 rows
 constexpr size_t narrow_lds_bytes(int eb, int tb, bool lw) {
     return static_cast<size_t>(waves_for(eb, tb)) * 16 * eb *
@@ -59,13 +64,6 @@ constexpr size_t narrow_lds_bytes(int eb, int tb, bool lw) {
 bool narrow_lds_weights(const void* w_gate, int H, int E) {
     return E % 8 == 0 && (reinterpret_cast<uintptr_t>(w_gate) & 15) == 0 &&
            static_cast<int64_t>(H) * E * 2 < (int64_t{1} << 31);
-}
-
-// Keeps the larger of two (probability, expert) candidates; an exact tie goes to the lower expert index.
-__device__ __forceinline__ void argmax_step(float& bv, int& bi, float ov, int oi) {
-    const bool take = (ov > bv) | ((ov == bv) & (oi < bi));  // no short circuit: two selects, no branch
-    bv = take ? ov : bv;
-    bi = take ? oi : bi;
 }
 
 // The 16-lane all-reduce runs on DPP row operations (a VALU operand modifier, no LDS round trip). Step 0 pairs
@@ -88,8 +86,8 @@ __device__ __forceinline__ float row_partner(float v) {
 // fixed association, identical in every lane of the row, so a token's result does not depend on its batch.
 // Probabilities are exp(l - max) / sum, the K picks come in descending order, and their renormalisation sums
 // them in rank order (the oracle's order, tests/moe_cpu_sim.cpp:224-243); lane gl writes picks gl, gl + 16, ...
-// below K. Padding experts (e >= E) and picked experts hold -2, below every probability. All 64 lanes of the
-// wave must call this (DPP reads the neighbours' registers); only rows with `active` set write.
+// below K. All 64 lanes of the wave must call this (DPP reads the neighbours' registers); only rows with
+// `active` set write.
 template <int EPL>
 __device__ __forceinline__ void select_row(const float* row, int E, int K, bool active, int32_t* ids_out,
                                            uint16_t* w_out) {
@@ -117,48 +115,56 @@ __device__ __forceinline__ void select_row(const float* row, int E, int K, bool 
     total += row_partner<1>(total);
     total += row_partner<2>(total);
     total += row_partner<3>(total);
+    // One 64-bit key per candidate: the probability's bits + 1 above, the complemented expert index below. For
+    // p >= 0 the bits order like the values, so the largest key is the largest probability and, among exact
+    // ties, the lowest index (the reference's strict '>' scan in index order). Padding experts, NaN and picked
+    // experts hold a zero upper word, below every candidate.
+    uint64_t key[EPL];
 #pragma unroll
-    for (int q = 0; q < EPL; ++q) v[q] = gl + G * q < E ? v[q] / total : -2.0f;
-    constexpr int NP = EPL;  // K <= E <= 16 EPL picks; pick k sits in lane k % 16, slot k / 16
-    float sel = 0.0f, my_p[NP];
-    int my_id[NP];
-#pragma unroll
-    for (int j = 0; j < NP; ++j) {
-        my_p[j] = 0.0f;
-        my_id[j] = 0;
+    for (int q = 0; q < EPL; ++q) {
+        const int e = gl + G * q;
+        const float pq = v[q] / total;
+        const uint32_t hi = e < E && pq == pq ? __builtin_bit_cast(uint32_t, pq) + 1u : 0u;  // NaN never wins
+        key[q] = (static_cast<uint64_t>(hi) << 32) | static_cast<uint32_t>(~e);
     }
+    constexpr int NP = EPL;  // K <= E <= 16 EPL picks; pick k sits in lane k % 16, slot k / 16
+    float sel = 0.0f;
+    uint64_t my_key[NP];
+#pragma unroll
+    for (int j = 0; j < NP; ++j) my_key[j] = 0;
     for (int k = 0; k < K; ++k) {
-        float bv = -3.0f;
-        int bi = 0x7fffffff;
+        uint64_t best = key[0];
 #pragma unroll
-        for (int q = 0; q < EPL; ++q) {  // q ascending: within a lane the lower index keeps an exact tie
-            if (v[q] > bv) {
-                bv = v[q];
-                bi = gl + G * q;
-            }
+        for (int q = 1; q < EPL; ++q) best = key[q] > best ? key[q] : best;
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            const uint32_t lo = static_cast<uint32_t>(best), hi = static_cast<uint32_t>(best >> 32);
+            const uint32_t olo = static_cast<uint32_t>(st == 0   ? row_partner<0>(static_cast<int>(lo))
+                                                       : st == 1 ? row_partner<1>(static_cast<int>(lo))
+                                                       : st == 2 ? row_partner<2>(static_cast<int>(lo))
+                                                                 : row_partner<3>(static_cast<int>(lo)));
+            const uint32_t ohi = static_cast<uint32_t>(st == 0   ? row_partner<0>(static_cast<int>(hi))
+                                                       : st == 1 ? row_partner<1>(static_cast<int>(hi))
+                                                       : st == 2 ? row_partner<2>(static_cast<int>(hi))
+                                                                 : row_partner<3>(static_cast<int>(hi)));
+            const uint64_t other = (static_cast<uint64_t>(ohi) << 32) | olo;
+            best = other > best ? other : best;
         }
-        argmax_step(bv, bi, row_partner<0>(bv), row_partner<0>(bi));
-        argmax_step(bv, bi, row_partner<1>(bv), row_partner<1>(bi));
-        argmax_step(bv, bi, row_partner<2>(bv), row_partner<2>(bi));
-        argmax_step(bv, bi, row_partner<3>(bv), row_partner<3>(bi));
 #pragma unroll
-        for (int q = 0; q < EPL; ++q)
-            if (gl + G * q == bi) v[q] = -2.0f;  // probabilities are >= 0: a picked expert never wins again
+        for (int q = 0; q < EPL; ++q)  // keys are unique (the index part): exactly one lane owns the pick
+            key[q] = key[q] == best ? static_cast<uint64_t>(static_cast<uint32_t>(key[q])) : key[q];
 #pragma unroll
-        for (int j = 0; j < NP; ++j) {
-            if ((k >> 4) == j && (k & (G - 1)) == gl) {  // the first test is uniform over the wave
-                my_id[j] = bi;
-                my_p[j] = bv;
-            }
-        }
-        sel += bv;
+        for (int j = 0; j < NP; ++j)
+            if ((k >> 4) == j && (k & (G - 1)) == gl) my_key[j] = best;  // the first test is uniform
+        sel += __builtin_bit_cast(float, static_cast<uint32_t>(best >> 32) - 1u);
     }
     if (active) {
 #pragma unroll
         for (int j = 0; j < NP; ++j) {
             if (gl + G * j < K) {
-                ids_out[gl + G * j] = my_id[j];
-                w_out[gl + G * j] = f32_to_f16_bits(my_p[j] / sel);
+                ids_out[gl + G * j] = static_cast<int32_t>(~static_cast<uint32_t>(my_key[j]));
+                const float pk = __builtin_bit_cast(float, static_cast<uint32_t>(my_key[j] >> 32) - 1u);
+                w_out[gl + G * j] = f32_to_f16_bits(pk / sel);
             }
         }
     }
@@ -485,7 +491,7 @@ hipError_t launch_narrow(const uint16_t* x, const uint16_t* w_gate, int32_t* ids
 template <int EB>
 hipError_t launch_eb(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H, int E,
                      int K, hipStream_t stream) {
-    switch (narrow_token_blocks(T)) {
+    switch (narrow_token_blocks(T, EB)) {
         case 1: return launch_narrow<EB, 1>(x, w_gate, ids, w, T, H, E, K, stream);
         case 2: return launch_narrow<EB, 2>(x, w_gate, ids, w, T, H, E, K, stream);
         default: return launch_narrow<EB, 4>(x, w_gate, ids, w, T, H, E, K, stream);
@@ -504,16 +510,16 @@ int routing_expert_blocks(int E) {
 }
 
 int routing_tokens_per_block(int T, int E) {
-    return routing_expert_blocks(E) <= 4 ? kTokensPerBlock * narrow_token_blocks(T) : kWideTokens;
+    return routing_expert_blocks(E) <= 4 ? kTokensPerBlock * narrow_token_blocks(T, routing_expert_blocks(E)) : kWideTokens;
 }
 int routing_block_threads(int T, int E) {
     const int eb = routing_expert_blocks(E);
-    return eb <= 4 ? waves_for(eb, narrow_token_blocks(T)) * kWave : kWideWaves * kWave;
+    return eb <= 4 ? waves_for(eb, narrow_token_blocks(T, eb)) * kWave : kWideWaves * kWave;
 }
 int routing_lds_bytes(int T, int E) {
     const int eb = routing_expert_blocks(E);
     if (eb > 4) return static_cast<int>(wide_lds_bytes(eb));
-    return static_cast<int>(narrow_lds_bytes(eb, narrow_token_blocks(T), E % 8 == 0));
+    return static_cast<int>(narrow_lds_bytes(eb, narrow_token_blocks(T, eb), E % 8 == 0));
 }
 
 hipError_t launch_routing_topk(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H,
