@@ -9,13 +9,16 @@ A step is one pass of the layer over one batch of synthetic input resident in HB
 through the C ABI of libmoe_mi355x.so on one stream, with caller-owned buffers allocated once.
 W warm-up steps, then five timed passes of K steps each, every pass between torch.cuda.synchronize() calls:
   1. eager: the three C-ABI calls per step, nothing else recorded -> `value` and `ms_per_step`;
-  2. graph replay: the same three calls captured once in a HIP graph, replayed W times untimed and then K times
-     (y checked bit-exact against the eager y first) -> `layer_us_graph_replay`;
+  2. graph replay: G layer steps (--graph-layers, default 10, as a serving loop captures a whole forward pass of
+     several MoE layers) captured once in a HIP graph, replayed untimed and then for K steps (y checked bit-exact
+     against the eager y first) -> `layer_us_graph_replay` per layer; one layer per graph ->
+     `layer_us_graph_replay_1`, which pays the ~9 us that separate consecutive graph launches once per layer;
   3. traced: eager again, with HIP events that the library records around each of its launches on the launch
      stream -> per-kernel average durations, from which `roofline` is computed.
-  4. fused: routing, then moe_expert_ffn_combine (the FFN and the combine in one call, an optional fast path;
-     expert_out and y checked bit-exact against the three-operator layer first, then W untimed steps)
-     -> `layer_us_fused_ffn_combine`.
+  4. fused: the whole layer in one library call, moe_layer (an optional fast path: on the tiled schedule the
+     routing kernel also ranks the slots for the FFN's permute, one launch fewer; on the streaming schedule the
+     combine runs in the down projection's reduce); ids, weights, expert_out and y checked bit-exact against the
+     three-operator layer first, then W untimed steps -> `layer_us_fused`.
      `value` stays the three-operator layer, the drop-in pipeline.
   5. per-step events: the three-operator layer with an event pair around every step ->
      `layer_us_per_step_events` (p10 / p50 / p90).
@@ -138,6 +141,7 @@ def main() -> int:
     ap.add_argument("--cpu-target-gflop", type=float, default=30.0,
                     help="size of the CPU baseline sample in GFLOP of expert FFN work")
     ap.add_argument("--no-graph", action="store_true", help="skip the HIP-graph replay timing")
+    ap.add_argument("--graph-layers", type=int, default=10, help="layer steps captured in one HIP graph")
     ap.add_argument("--no-prefill", action="store_true",
                     help="skip the T=8192 prefill pass that the decode workload adds (prefill_* keys)")
     ap.add_argument("--no-copy-rate", action="store_true",
@@ -210,48 +214,73 @@ def main() -> int:
     # 1) the layer as three eager C-ABI calls per step: the headline value
     ms_per_step, gpu_ms_per_step = timed(step)
     progress(f"eager: {ms_per_step * 1e3:.1f} us/step (host clock), {gpu_ms_per_step * 1e3:.1f} us/step (events)")
-    # 2) the same three calls captured once in a HIP graph and replayed (no memset nodes: the library records
-    #    kernels only); every replay recomputes the whole layer, and its y must equal the eager y bit for bit
-    graph_ms = None
+    # 2) the same three calls captured in a HIP graph and replayed (no memset nodes: the library records kernels
+    #    only); every replay recomputes the whole layer, and its y must equal the eager y bit for bit. Consecutive
+    #    graph launches are ~9 us apart on the GPU, so the graph holds G layer steps, as a whole forward pass would;
+    #    one layer per graph is timed too.
+    graph_ms = graph1_ms = None
     if not args.no_graph:
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            step(int(torch.cuda.current_stream().cuda_stream))
-        y.zero_()
-        g.replay()
-        torch.cuda.synchronize()
-        if not torch.equal(y, y_eager):
-            raise RuntimeError("graph replay of the layer differs from the eager layer")
-        # as many untimed replays as the eager pass had warm-up steps: after the capture and the synchronisations
-        # the shader clock has dropped, and it takes ~15 launches of the prefill GEMMs to ramp back up
-        for _ in range(args.warmup):
+        def graph_of(layers: int) -> "torch.cuda.CUDAGraph":
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for _ in range(layers):
+                    step(int(torch.cuda.current_stream().cuda_stream))
+            y.zero_()
             g.replay()
-        graph_ms, _ = timed(g.replay)
-        progress(f"graph replay: {graph_ms * 1e3:.1f} us/step (host clock)")
+            torch.cuda.synchronize()
+            if not torch.equal(y, y_eager):
+                raise RuntimeError("graph replay of the layer differs from the eager layer")
+            return g
+
+        def replay_ms(g, layers: int) -> float:
+            # untimed replays first: after the capture and the synchronisations the shader clock has dropped, and
+            # it takes ~15 launches of the prefill GEMMs to ramp back up
+            for _ in range(max(1, args.warmup // layers)):
+                g.replay()
+            reps = max(1, args.steps // layers)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                g.replay()
+            torch.cuda.synchronize()
+            return (time.perf_counter() - t0) * 1e3 / (reps * layers)
+
+        G = max(1, args.graph_layers)
+        g = graph_of(G)
+        graph_ms = replay_ms(g, G)
         del g
+        g = graph_of(1)
+        graph1_ms = replay_ms(g, 1)
+        del g
+        progress(f"graph replay: {graph_ms * 1e3:.1f} us/layer with {G} layers per graph, "
+                 f"{graph1_ms * 1e3:.1f} us/layer with one (host clock)")
     # 3) per-kernel HIP events recorded by the library on the launch stream: durations for the roofline
     with ops.kernel_trace() as kernels:
         traced_ms, _ = timed(step)
     progress(f"traced: {traced_ms * 1e3:.1f} us/step with an event pair around every launch")
-    # 4) the optional fast path: routing, then the FFN and the combine in one call (moe_expert_ffn_combine);
-    #    y and expert_out must equal the three-operator layer's bit for bit
+    # 4) the optional fast path: the whole layer in one call (moe_layer); ids, weights, expert_out and y must
+    #    equal the three-operator layer's bit for bit
+    ws_layer_bytes = ops.layer_workspace_bytes(T, H, E, K, I)
+    ws_layer = torch.empty(ws_layer_bytes, dtype=torch.uint8, device=dev)
+
     def step_fused(s: int = sp) -> None:
-        st = lib.moe_routing_topk(p["x"], p["wg"], p["ids"], p["w"], T, H, E, K, s)
-        st |= lib.moe_expert_ffn_combine(p["x"], p["ids"], p["w"], p["ew"], p["eo"], p["y"], p["ws"], ws_bytes,
-                                         T, H, E, K, I, s)
+        st = lib.moe_layer(p["x"], p["wg"], p["ew"], p["ids"], p["w"], p["eo"], p["y"], ws_layer.data_ptr(),
+                           ws_layer_bytes, T, H, E, K, I, s)
         if st:
             raise RuntimeError(lib.moe_last_error().decode())
 
-    eo_eager = eo.clone()
+    eo_eager, ids_eager, w_eager = eo.clone(), ids.clone(), w.clone()
     y.zero_()
+    eo.zero_()
     step_fused()
     torch.cuda.synchronize()
-    if not (torch.equal(y, y_eager) and torch.equal(eo, eo_eager)):
-        raise RuntimeError("the fused FFN + combine differs from the three-operator layer")
+    if not (torch.equal(y, y_eager) and torch.equal(eo, eo_eager) and torch.equal(ids, ids_eager)
+            and torch.equal(w, w_eager)):
+        raise RuntimeError("the fused layer (moe_layer) differs from the three-operator layer")
     for _ in range(args.warmup):  # the check above left the GPU idle: let the clock ramp up again
         step_fused()
     fused_ms, fused_gpu_ms = timed(step_fused)
-    progress(f"fused FFN + combine: {fused_ms * 1e3:.1f} us/step (host clock), {fused_gpu_ms * 1e3:.1f} us/step (events)")
+    progress(f"fused layer (moe_layer): {fused_ms * 1e3:.1f} us/step (host clock), {fused_gpu_ms * 1e3:.1f} us/step (events)")
     # 5) per-step spread of the three-operator layer: an event pair around every step
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
     torch.cuda.synchronize()
@@ -430,8 +459,10 @@ def main() -> int:
                    "hidden": H, "experts": E, "top_k": K, "intermediate": I, "active_experts": active},
         "layer_us_gpu_events": round(gpu_ms_per_step * 1e3, 2),
         "layer_us_graph_replay": round(graph_ms * 1e3, 2) if graph_ms else None,
+        "graph_layers_per_replay": max(1, args.graph_layers) if graph_ms else None,
+        "layer_us_graph_replay_1": round(graph1_ms * 1e3, 2) if graph1_ms else None,
         "layer_us_traced": round(traced_ms * 1e3, 2),
-        "layer_us_fused_ffn_combine": round(fused_ms * 1e3, 2),
+        "layer_us_fused": round(fused_ms * 1e3, 2),
         "layer_us_per_step_events": spread,
         "ffn_us": round(ffn_ms * 1e3, 2),
         "ffn_tflops": round(ffn_flops / (ffn_ms * 1e-3) / 1e12, 2),

@@ -69,6 +69,8 @@ SIGNATURES = {
     "moe_expert_ffn": (_I32, [_P, _P, _P, _P, _P, _P, C.c_size_t, _I64, _I64, _I64, _I64, _I64, _P]),
     "moe_expert_ffn_combine": (_I32, [_P, _P, _P, _P, _P, _P, _P, C.c_size_t, _I64, _I64, _I64, _I64, _I64, _P]),
     "moe_expert_ffn_no_alloc": (_I32, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P]),
+    "moe_layer_workspace_bytes": (C.c_size_t, [_I64, _I64, _I64, _I64, _I64]),
+    "moe_layer": (_I32, [_P, _P, _P, _P, _P, _P, _P, _P, C.c_size_t, _I64, _I64, _I64, _I64, _I64, _P]),
     "moe_combine_infer_shape": (_I32, [_I64P, _I32, _I64P, _I32, _I64P]),
     "moe_combine_infer_dtype": (_I32, [C.POINTER(_I32)]),
     "moe_combine_plan_for": (_I32, [_I64, _I64, _I64, C.POINTER(CombinePlan)]),

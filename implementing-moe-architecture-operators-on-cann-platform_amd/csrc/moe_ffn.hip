@@ -13,6 +13,7 @@
 
 #include "moe_device.h"
 #include "moe_launch.h"
+#include "moe_slot_rank.h"
 
 namespace moe {
 
@@ -135,6 +136,45 @@ hipError_t launch_ffn_combine(const uint16_t* x, const int32_t* expert_ids, cons
     const hipError_t err = launch_ffn(x, expert_ids, expert_weights, expert_out, ws, T, H, E, K, I, stream);
     if (err != hipSuccess) return err;
     return launch_combine(expert_out, weights, y, T, H, K, stream);
+}
+
+size_t layer_workspace_bytes(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
+    size_t bytes = ffn_workspace_bytes(T, H, E, K, I);
+    if (ffn_schedule(T, H, E, K, I) == 1)
+        bytes += align_up(sizeof(int32_t) * static_cast<size_t>(routing_blocks(static_cast<int>(T), static_cast<int>(E))) *
+                              counts_stride(static_cast<int>(E)),
+                          256);
+    return bytes;
+}
+
+hipError_t launch_layer(const uint16_t* x, const uint16_t* w_gate, const uint16_t* expert_weights, int32_t* ids,
+                        uint16_t* weights, uint16_t* expert_out, uint16_t* y, void* workspace, int T, int H, int E,
+                        int K, int I, hipStream_t stream) {
+    const FfnWorkspace ws = ffn_workspace_carve(workspace, T, H, E, K, I);
+    switch (ffn_schedule(T, H, E, K, I)) {
+        case 1: {
+            hipError_t err = prepare_ffn_tiled();
+            if (err != hipSuccess) return err;
+            // rank [T*K] in the permute's scratch; the routing blocks' counts after the FFN workspace
+            int32_t* rank = ws.pscratch;
+            int32_t* counts = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + ffn_workspace_bytes(T, H, E, K, I));
+            err = launch_routing_topk(x, w_gate, ids, weights, T, H, E, K, stream, counts, rank);
+            if (err != hipSuccess) return err;
+            const int nblocks = routing_blocks(T, E);
+            err = launch_permute_scatter(ids, T * K, E, H, counts, rank, nblocks, routing_tokens_per_block(T, E) * K,
+                                         permute_scatter_chunks_per_block(nblocks), ws, expert_out, stream);
+            if (err != hipSuccess) return err;
+            err = launch_ffn_tiled(x, expert_weights, expert_out, ws, T, H, E, K, I, stream, /*allow_split=*/true);
+            if (err != hipSuccess) return err;
+            return launch_combine(expert_out, weights, y, T, H, K, stream);
+        }
+        case 0: {
+            const hipError_t err = launch_routing_topk(x, w_gate, ids, weights, T, H, E, K, stream);
+            if (err != hipSuccess) return err;
+            return launch_ffn_combine(x, ids, weights, expert_weights, expert_out, y, ws, T, H, E, K, I, stream);
+        }
+        default: return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace moe

@@ -36,8 +36,12 @@ int routing_expert_blocks(int E);
 int routing_tokens_per_block(int T, int E);
 int routing_block_threads(int T, int E);
 int routing_lds_bytes(int T, int E);
+int routing_blocks(int T, int E);  // workgroups of a routing launch; each routes routing_tokens_per_block tokens
+// counts/rank non-null: the kernel's tail also ranks each block's slots by expert (rank[T*K]) and writes the
+// block's per-expert counts (counts[routing_blocks][counts_stride(E)], 16-byte aligned), the permute's first half
 hipError_t launch_routing_topk(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H,
-                               int E, int K, hipStream_t stream);
+                               int E, int K, hipStream_t stream, int32_t* counts = nullptr,
+                               int32_t* rank = nullptr);
 
 // ---- expert FFN (moe_permute.hip, moe_ffn.hip) ----
 struct FfnWorkspace {
@@ -58,6 +62,12 @@ int permute_block_threads();
 int permute_chunks(int S);
 size_t permute_scratch_bytes(int S, int E);
 hipError_t prepare_permute(int S, int E);  // kernel attributes, before the first launch of a call
+// the scatter alone, over chunk counts and ranks some other kernel wrote (counts rows of counts_stride(E) ints,
+// 16-byte aligned; chunk c holds the slots [c chunk_slots, (c + 1) chunk_slots)), cpw chunks per workgroup
+int permute_scatter_chunks_per_block(int nchunks);
+hipError_t launch_permute_scatter(const int32_t* ids, int S, int E, int H, const int32_t* counts,
+                                  const int32_t* rank, int nchunks, int chunk_slots, int cpw, FfnWorkspace ws,
+                                  uint16_t* expert_out, hipStream_t stream);
 hipError_t launch_permute(const int32_t* ids, int S, int E, int H, FfnWorkspace ws, uint16_t* expert_out,
                           hipStream_t stream);
 
@@ -110,6 +120,16 @@ hipError_t launch_ffn(const uint16_t* x, const int32_t* expert_ids, const uint16
 hipError_t launch_ffn_combine(const uint16_t* x, const int32_t* expert_ids, const uint16_t* weights,
                               const uint16_t* expert_weights, uint16_t* expert_out, uint16_t* y, FfnWorkspace ws,
                               int T, int H, int E, int K, int I, hipStream_t stream);
+
+// ---- the whole layer: routing -> FFN -> combine in one call (moe_ffn.hip) ----
+// workspace: the FFN's (ffn_workspace_bytes), then on the tiled schedule the routing blocks' expert counts
+size_t layer_workspace_bytes(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I);
+// Tiled schedule: the routing kernel also ranks its blocks' slots (the permute's count), then one scatter launch,
+// the two GEMMs and the combine. Streaming schedule: routing, then launch_ffn_combine. ids, weights, expert_out
+// and y equal the three operators' bit for bit.
+hipError_t launch_layer(const uint16_t* x, const uint16_t* w_gate, const uint16_t* expert_weights, int32_t* ids,
+                        uint16_t* weights, uint16_t* expert_out, uint16_t* y, void* workspace, int T, int H, int E,
+                        int K, int I, hipStream_t stream);
 
 // ---- fixed scratch of the allocation-free FFN entry point (moe_noalloc.hip) ----
 size_t noalloc_scratch_bytes();

@@ -318,6 +318,36 @@ moe_status moe_expert_ffn_combine(const uint16_t* x, const int32_t* expert_ids, 
     return ok();
 }
 
+// The whole layer in one call (optional fast path; the three operators stay the contract)
+size_t moe_layer_workspace_bytes(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
+    if (check_ffn_sizes(T, H, E, K, I) != MOE_OK) return 0;
+    return moe::layer_workspace_bytes(T, H, E, K, I);
+}
+
+moe_status moe_layer(const uint16_t* x, const uint16_t* w_gate, const uint16_t* expert_weights, int32_t* expert_ids,
+                     uint16_t* weights, uint16_t* expert_out, uint16_t* y, void* workspace, size_t workspace_bytes,
+                     int64_t T, int64_t H, int64_t E, int64_t K, int64_t I, void* stream) {
+    moe_status st = check_ffn_sizes(T, H, E, K, I);  // includes the routing checks
+    if (st != MOE_OK) return st;
+    st = check_combine_sizes(T, H, K);
+    if (st != MOE_OK) return st;
+    if (T == 0) return ok();
+    if (!x || !w_gate || !expert_weights || !expert_ids || !weights || !expert_out || !y)
+        return fail(MOE_ERR_NULL, "MoE layer: null tensor pointer");
+    const size_t need = moe::layer_workspace_bytes(T, H, E, K, I);
+    if (!workspace || workspace_bytes < need)
+        return fail(MOE_ERR_WORKSPACE, "MoE layer: workspace %zu bytes at %p, need %zu", workspace_bytes, workspace,
+                    need);
+    if (!aligned16(x) || !aligned16(expert_weights) || !aligned16(expert_out) || !aligned16(workspace) ||
+        !aligned16(y))
+        return fail(MOE_ERR_UNSUPPORTED, "MoE layer: x, expert_weights, expert_out, y, workspace must be 16-byte aligned");
+    const hipError_t err = moe::launch_layer(x, w_gate, expert_weights, expert_ids, weights, expert_out, y, workspace,
+                                             static_cast<int>(T), static_cast<int>(H), static_cast<int>(E),
+                                             static_cast<int>(K), static_cast<int>(I), as_stream(stream));
+    if (err != hipSuccess) return hip_fail(err, "MoE layer launch");
+    return ok();
+}
+
 // ------------------------------------------------------------------------------------------------
 // MoeCombine
 // ------------------------------------------------------------------------------------------------

@@ -29,6 +29,7 @@
 
 #include "moe_device.h"
 #include "moe_launch.h"
+#include "moe_slot_rank.h"
 
 namespace moe {
 
@@ -195,7 +196,9 @@ __global__ __launch_bounds__(waves_for(EB, TB) * kWave) void routing_topk_kernel
                                                                               const uint16_t* __restrict__ w_gate,
                                                                               int32_t* __restrict__ expert_ids,
                                                                               uint16_t* __restrict__ weights, int T,
-                                                                              int H, int E, int K) {
+                                                                              int H, int E, int K,
+                                                                              int32_t* __restrict__ counts,
+                                                                              int32_t* __restrict__ rank) {
     constexpr int W = waves_for(EB, TB);
     constexpr int U = unroll_for(EB, TB);
     constexpr int Epad = EB * 16;
@@ -333,7 +336,15 @@ __global__ __launch_bounds__(waves_for(EB, TB) * kWave) void routing_topk_kernel
         const bool active = t < NT && t0 + t < T;
         const int tr = min(t, NT - 1);  // inactive groups read a valid row and write nothing
         select_row<EB>(part + tr * Epad, E, K, active, expert_ids + static_cast<size_t>(t0 + tr) * K,
-                                    weights + static_cast<size_t>(t0 + tr) * K);
+                       weights + static_cast<size_t>(t0 + tr) * K);
+    }
+    // ---- optional tail: the block's slots ranked by expert, for the permute's scatter ----
+    if (counts != nullptr) {
+        __syncthreads();  // the block's ids are written and part[] is no longer read
+        constexpr int MAXIT = (NT * kMaxTopK + W * kWave - 1) / (W * kWave);
+        rank_slots<W, MAXIT>(expert_ids, t0 * K, min(T, t0 + NT) * K, E, counts_stride(E),
+                             reinterpret_cast<int*>(part), counts + static_cast<size_t>(blockIdx.x) * counts_stride(E),
+                             rank);
     }
 }
 
@@ -350,7 +361,9 @@ __global__ __launch_bounds__(kWideWaves * kWave) void routing_wide_kernel(const 
                                                                            const uint16_t* __restrict__ w_gate,
                                                                            int32_t* __restrict__ expert_ids,
                                                                            uint16_t* __restrict__ weights, int T,
-                                                                           int H, int E, int K) {
+                                                                           int H, int E, int K,
+                                                                           int32_t* __restrict__ counts,
+                                                                           int32_t* __restrict__ rank) {
     constexpr int Epad = EB * 16;
     constexpr int CH = wide_chunks(EB);
     constexpr int P = wide_pitch(EB);
@@ -443,9 +456,16 @@ __global__ __launch_bounds__(kWideWaves * kWave) void routing_wide_kernel(const 
     for (int tb = wave * TPW; tb < kWideTokens; tb += kWideWaves * TPW) {
         const int t = tb + lane / kSelLanes;
         const bool active = t0 + t < T;
-        select_row<EB>(logits + t * Epad, E, K, active,
-                                    expert_ids + static_cast<size_t>(active ? t0 + t : 0) * K,
-                                    weights + static_cast<size_t>(active ? t0 + t : 0) * K);
+        select_row<EB>(logits + t * Epad, E, K, active, expert_ids + static_cast<size_t>(active ? t0 + t : 0) * K,
+                       weights + static_cast<size_t>(active ? t0 + t : 0) * K);
+    }
+    // ---- optional tail: the block's slots ranked by expert, for the permute's scatter ----
+    if (counts != nullptr) {
+        __syncthreads();  // the block's ids are written and the logits are no longer read
+        constexpr int MAXIT = (kWideTokens * kMaxTopK + kWideWaves * kWave - 1) / (kWideWaves * kWave);
+        rank_slots<kWideWaves, MAXIT>(expert_ids, t0 * K, min(T, t0 + kWideTokens) * K, E, counts_stride(E),
+                                      reinterpret_cast<int*>(logits),
+                                      counts + static_cast<size_t>(blockIdx.x) * counts_stride(E), rank);
     }
 }
 
@@ -457,44 +477,46 @@ size_t wide_lds_bytes(int eb) {
 
 template <int EB>
 hipError_t launch_wide(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H, int E,
-                       int K, hipStream_t stream) {
+                       int K, int32_t* counts, int32_t* rank, hipStream_t stream) {
     const int grid = (T + kWideTokens - 1) / kWideTokens;
     const size_t lds = wide_lds_bytes(EB);
     const hipError_t attr = ensure_lds_limit(reinterpret_cast<const void*>(&routing_wide_kernel<EB>),
                                              static_cast<int>(lds));
     if (attr != hipSuccess) return attr;
     TraceScope trace("moe_routing_topk", stream);
-    routing_wide_kernel<EB><<<grid, kWideWaves * kWave, lds, stream>>>(x, w_gate, ids, w, T, H, E, K);
+    routing_wide_kernel<EB><<<grid, kWideWaves * kWave, lds, stream>>>(x, w_gate, ids, w, T, H, E, K, counts, rank);
     return hipGetLastError();
 }
 
 template <int EB, int TB, bool LW>
 hipError_t launch_narrow(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H, int E,
-                         int K, hipStream_t stream) {
+                         int K, int32_t* counts, int32_t* rank, hipStream_t stream) {
     const int grid = (T + 16 * TB - 1) / (16 * TB);
     const size_t lds = narrow_lds_bytes(EB, TB, LW);
     const hipError_t attr = ensure_lds_limit(reinterpret_cast<const void*>(&routing_topk_kernel<EB, TB, LW>),
                                              static_cast<int>(lds));
     if (attr != hipSuccess) return attr;
     TraceScope trace("moe_routing_topk", stream);
-    routing_topk_kernel<EB, TB, LW><<<grid, waves_for(EB, TB) * kWave, lds, stream>>>(x, w_gate, ids, w, T, H, E, K);
+    routing_topk_kernel<EB, TB, LW><<<grid, waves_for(EB, TB) * kWave, lds, stream>>>(x, w_gate, ids, w, T, H, E, K,
+                                                                                    counts, rank);
     return hipGetLastError();
 }
 
 template <int EB, int TB>
 hipError_t launch_narrow(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H, int E,
-                         int K, hipStream_t stream) {
-    return narrow_lds_weights(w_gate, H, E) ? launch_narrow<EB, TB, true>(x, w_gate, ids, w, T, H, E, K, stream)
-                                            : launch_narrow<EB, TB, false>(x, w_gate, ids, w, T, H, E, K, stream);
+                         int K, int32_t* counts, int32_t* rank, hipStream_t stream) {
+    return narrow_lds_weights(w_gate, H, E)
+               ? launch_narrow<EB, TB, true>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream)
+               : launch_narrow<EB, TB, false>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);
 }
 
 template <int EB>
 hipError_t launch_eb(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H, int E,
-                     int K, hipStream_t stream) {
+                     int K, int32_t* counts, int32_t* rank, hipStream_t stream) {
     switch (narrow_token_blocks(T, EB)) {
-        case 1: return launch_narrow<EB, 1>(x, w_gate, ids, w, T, H, E, K, stream);
-        case 2: return launch_narrow<EB, 2>(x, w_gate, ids, w, T, H, E, K, stream);
-        default: return launch_narrow<EB, 4>(x, w_gate, ids, w, T, H, E, K, stream);
+        case 1: return launch_narrow<EB, 1>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);
+        case 2: return launch_narrow<EB, 2>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);
+        default: return launch_narrow<EB, 4>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);
     }
 }
 
@@ -522,14 +544,19 @@ int routing_lds_bytes(int T, int E) {
     return static_cast<int>(narrow_lds_bytes(eb, narrow_token_blocks(T, eb), E % 8 == 0));
 }
 
+int routing_blocks(int T, int E) {
+    const int tpb = routing_tokens_per_block(T, E);
+    return (T + tpb - 1) / tpb;
+}
+
 hipError_t launch_routing_topk(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H,
-                               int E, int K, hipStream_t stream) {
+                               int E, int K, hipStream_t stream, int32_t* counts, int32_t* rank) {
     switch (routing_expert_blocks(E)) {
-        case 1: return launch_eb<1>(x, w_gate, ids, w, T, H, E, K, stream);
-        case 2: return launch_eb<2>(x, w_gate, ids, w, T, H, E, K, stream);
-        case 4: return launch_eb<4>(x, w_gate, ids, w, T, H, E, K, stream);
-        case 8: return launch_wide<8>(x, w_gate, ids, w, T, H, E, K, stream);
-        default: return launch_wide<16>(x, w_gate, ids, w, T, H, E, K, stream);
+        case 1: return launch_eb<1>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);
+        case 2: return launch_eb<2>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);
+        case 4: return launch_eb<4>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);
+        case 8: return launch_wide<8>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);
+        default: return launch_wide<16>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);
     }
 }
 

@@ -79,6 +79,10 @@ def workspace_bytes(T: int, H: int, E: int, K: int, I: int) -> int:
     return int(_lib.load().moe_expert_ffn_workspace_bytes(T, H, E, K, I))
 
 
+def layer_workspace_bytes(T: int, H: int, E: int, K: int, I: int) -> int:
+    return int(_lib.load().moe_layer_workspace_bytes(T, H, E, K, I))
+
+
 def MoeRoutingTopK(x: torch.Tensor, w_gate: torch.Tensor, topK: int = 2, stream=None):
     """x[T,H] fp16, w_gate[H,E] fp16 -> (expert_ids[T,K] int32, weights[T,K] fp16)."""
     _need(x, "x", torch.float16)
@@ -176,6 +180,34 @@ def moe_layer(x: torch.Tensor, w_gate: torch.Tensor, expert_weights: torch.Tenso
     eo = MoeExpertFFN(x, ids, w, expert_weights, 0, workspace, stream=stream)
     y = MoeCombine(eo, ids, w, topK, stream=stream)
     return y, ids, w, eo
+
+
+def moe_layer_fused(x: torch.Tensor, w_gate: torch.Tensor, expert_weights: torch.Tensor, topK: int = 2,
+                    intermediateSize: int = 0, workspace: torch.Tensor | None = None, stream=None):
+    """The whole layer in one library call (moe_layer): the routing kernel also ranks the slots for the FFN's
+    permute. Returns (y, expert_ids, weights, expert_out), bit-identical to moe_layer's."""
+    _need(x, "x", torch.float16)
+    _need(w_gate, "w_gate", torch.float16)
+    _need(expert_weights, "expert_weights", torch.float16)
+    (ids_shape, ids_dt), (w_shape, w_dt) = infer_routing(tuple(x.shape), tuple(w_gate.shape), topK)
+    out_shape, out_dt, inter = infer_expert_ffn(tuple(x.shape), ids_shape, tuple(expert_weights.shape),
+                                                intermediateSize)
+    T, H = x.shape
+    E, K = expert_weights.shape[0], ids_shape[1]
+    need = layer_workspace_bytes(T, H, E, K, inter)
+    s = _stream(stream)
+    with torch.cuda.stream(s):
+        if workspace is None:
+            workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
+        ids = torch.empty(ids_shape, dtype=ids_dt, device=x.device)
+        w = torch.empty(w_shape, dtype=w_dt, device=x.device)
+        expert_out = torch.empty(out_shape, dtype=out_dt, device=x.device)
+        y = torch.empty((T, H), dtype=torch.float16, device=x.device)
+    check(_lib.load().moe_layer(x.data_ptr(), w_gate.data_ptr(), expert_weights.data_ptr(), ids.data_ptr(),
+                                w.data_ptr(), expert_out.data_ptr(), y.data_ptr(), workspace.data_ptr(),
+                                workspace.numel() * workspace.element_size(), T, H, E, K, inter,
+                                int(s.cuda_stream)))
+    return y, ids, w, expert_out
 
 
 def synth_normal_f16_(out: torch.Tensor, seed: int, stream_id: int, sigma_a: float, sigma_b: float | None = None,

@@ -203,6 +203,24 @@ moe_status moe_expert_ffn_combine(const uint16_t* x, const int32_t* expert_ids, 
                                   void* workspace, size_t workspace_bytes, int64_t num_tokens, int64_t hidden_size,
                                   int64_t num_experts, int64_t top_k, int64_t intermediate_size, void* stream);
 
+/* ------------------------------------------------------------------------------------------------------
+ * Optional fast path: the whole layer, MoeRoutingTopK -> MoeExpertFFN -> MoeCombine, in one call. It has no
+ * single counterpart in the reference, whose harness chains the three operators (tests/test_moe.cpp:520-612:
+ * routing, FFN, combine on one stream); the three operators stay the contract. On the LDS-tiled schedule the
+ * routing kernel also ranks each token block's (token, k) slots by expert, so the FFN's permute is a single
+ * scatter launch after it (the per-expert id scan of op_kernel/moe_expert_ffn.cpp:182-195, done once); on the
+ * weight-streaming schedule it is routing followed by moe_expert_ffn_combine. expert_ids, weights, expert_out
+ * and y are bit-identical to the three calls'. Deterministic (no atomics).
+ * The workspace is moe_layer_workspace_bytes() (>= moe_expert_ffn_workspace_bytes()); 0 = unsupported sizes.
+ * Sizes and errors as the three operators' checks together.
+ * ---------------------------------------------------------------------------------------------------- */
+size_t moe_layer_workspace_bytes(int64_t num_tokens, int64_t hidden_size, int64_t num_experts, int64_t top_k,
+                                 int64_t intermediate_size);
+moe_status moe_layer(const uint16_t* x, const uint16_t* w_gate, const uint16_t* expert_weights,
+                     int32_t* expert_ids, uint16_t* weights, uint16_t* expert_out, uint16_t* y, void* workspace,
+                     size_t workspace_bytes, int64_t num_tokens, int64_t hidden_size, int64_t num_experts,
+                     int64_t top_k, int64_t intermediate_size, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -172,6 +172,16 @@ def test_launch_argument_errors_return_before_launch(lib):
     assert fused(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE + 2, FAKE, need, *args) == ERR_UNSUP  # misaligned y
     assert fused(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, need, 4, 64, 4, 5, 256, None) == ERR_ARG
     assert fused(None, None, None, None, None, None, None, 0, 0, 64, 4, 2, 256, None) == MOE_OK  # T = 0
+    # the whole layer checks the three operators' rules and its own workspace before any launch
+    lneed = lib.moe_layer_workspace_bytes(4, 64, 4, 2, 256)
+    assert lneed >= need
+    layer = lib.moe_layer
+    assert layer(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, lneed - 1, *args) == ERR_WS
+    assert layer(FAKE, None, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, lneed, *args) == ERR_NULL  # w_gate
+    assert layer(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE + 2, FAKE, lneed, *args) == ERR_UNSUP  # misaligned y
+    assert layer(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, lneed, 4, 64, 4, 5, 256, None) == ERR_ARG
+    assert layer(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, lneed, 4, 60, 4, 2, 256, None) == ERR_UNSUP
+    assert layer(None, None, None, None, None, None, None, None, 0, 0, 64, 4, 2, 256, None) == MOE_OK  # T = 0
     assert lib.moe_combine(None, None, None, None, 4, 64, 2, None) == ERR_NULL
     assert lib.moe_combine(FAKE, None, FAKE, FAKE, 4, 60, 2, None) == ERR_UNSUP
     assert lib.moe_combine(FAKE, None, FAKE, FAKE, 4, 64, 0, None) == ERR_ARG
@@ -179,6 +189,17 @@ def test_launch_argument_errors_return_before_launch(lib):
     assert lib.moe_copy_bytes(FAKE, FAKE, 17, None) == ERR_ARG
     assert lib.moe_stream_read_bytes(None, 16384, None) == ERR_NULL
     assert lib.moe_stream_read_bytes(FAKE, 16000, None) == ERR_ARG
+
+
+def test_layer_workspace_adds_the_routing_counts_on_the_tiled_schedule(lib):
+    # streaming schedule (decode): the FFN's workspace as it is
+    assert lib.moe_layer_workspace_bytes(128, 2048, 16, 2, 8192) == lib.moe_expert_ffn_workspace_bytes(128, 2048, 16, 2, 8192)
+    # tiled schedule: + one row of counts_stride(E) int32 per routing workgroup, 256-byte aligned
+    for T, E, blocks in ((16384, 64, 512), (8192, 16, 256), (3000, 130, 47)):
+        ffn = lib.moe_expert_ffn_workspace_bytes(T, 2048, E, 6, 1408)
+        extra = (blocks * ((E + 3) // 4 * 4) * 4 + 255) // 256 * 256
+        assert lib.moe_layer_workspace_bytes(T, 2048, E, 6, 1408) == ffn + extra, (T, E)
+    assert lib.moe_layer_workspace_bytes(128, 2048, 16, 2, 8200) == 0  # I % 32 != 0
 
 
 def test_last_error_is_cleared_on_success(lib):

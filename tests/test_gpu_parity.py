@@ -167,7 +167,8 @@ def test_layer_empty_and_single_token(ops):
 @pytest.mark.parametrize("T,H,E,K,I,schedule", [(64, 256, 8, 2, 512, 0), (512, 256, 4, 2, 512, 1)])
 def test_layer_graph_replay_matches_eager(ops, T, H, E, K, I, schedule):
     """The layer's three C-ABI calls captured in one HIP graph: each replay, after eager work that changes x and
-    clears the graph's outputs, equals an eager run on the same x bit for bit (ids, weights, expert_out, y)."""
+    clears the graph's outputs, equals an eager run on the same x bit for bit (ids, weights, expert_out, y), and
+    the replay's own outputs pass the oracle checks (routing, the expert FFN, the combine bit for bit)."""
     lib = ops._lib.load()
     log(f"[graph] T={T} H={H} E={E} K={K} I={I} schedule={ffn_schedule(T, H, E, K, I)}")
     gen = torch.Generator(device="cpu").manual_seed(T + I)
@@ -208,6 +209,14 @@ def test_layer_graph_replay_matches_eager(ops, T, H, E, K, I, schedule):
         torch.cuda.synchronize()
         for name in ("ids", "w", "eo", "y"):
             assert torch.equal(gb[name], eb[name]), (i, name)
+        ids, w = host(gb["ids"]), host(gb["w"])
+        xh = host(x)
+        check_routing(ids, w, xh, host(wg), K, f"graph replay {i}")
+        eo = f32(host(gb["eo"]))
+        within(oracle.compare(eo, oracle.expert_ffn(f32(xh), ids, f32(host(ew)), I)), max_abs=1e-2, mean_abs=1e-3,
+               cos=0.9999)
+        y_o = oracle.combine(eo, f32(w)).astype(np.float16)
+        assert np.array_equal(host(gb["y"]).view(np.uint16), y_o.view(np.uint16)), i
     del g
 
 
@@ -707,6 +716,45 @@ def test_layer_on_a_side_stream(ops):
         for a, b in zip(ref, got):
             assert torch.equal(a, b)
         assert torch.equal(eo_f, eo_s) and torch.equal(y_f, y_s)
+
+
+@pytest.mark.parametrize("T,H,E,K,I,schedule", [
+    (64, 256, 8, 2, 512, 0),       # weight streaming: routing, then the FFN with the combine in its reduce
+    (1000, 128, 8, 2, 128, 1),     # tiled; routing 16-token blocks of 16 waves, w_gate through LDS
+    (2100, 128, 20, 3, 128, 1),    # E % 8 != 0: w_gate by 2-byte loads; 32 experts' blocks
+    (9000, 128, 64, 6, 128, 1),    # two 16-token blocks per workgroup, 192 slots per count chunk
+    (17000, 128, 13, 2, 128, 1),   # four 16-token blocks; E % 4 != 0 pads the counts rows
+    (3000, 128, 130, 4, 128, 1),   # E > 64: the wide routing kernel counts its 64 tokens
+])
+def test_fused_layer_matches_oracle_and_operators(ops, T, H, E, K, I, schedule):
+    """moe_layer (routing that also ranks its blocks' slots, one scatter launch, the FFN, the combine): ids and
+    weights pass the oracle's routing check on every token; the workspace's offsets and sorted_slot equal a stable
+    sort of those ids; expert_out matches the oracle FFN on a token sample and y is the oracle combine of it bit
+    for bit; and every output equals the three operators' run bit for bit."""
+    assert ffn_schedule(T, H, E, K, I) == schedule
+    log(f"[fused layer] T={T} H={H} E={E} K={K} I={I} schedule={schedule}")
+    rng = np.random.default_rng(T + E)
+    x = rng.standard_normal((T, H)).astype(np.float16)
+    wg = (rng.standard_normal((H, E)) / math.sqrt(H)).astype(np.float16)
+    ew = (rng.standard_normal((E, 3 * I, H)) / math.sqrt(H)).astype(np.float16)
+    x_d, wg_d, ew_d = dev(x), dev(wg), dev(ew)
+    ws = torch.empty(ops.layer_workspace_bytes(T, H, E, K, I), dtype=torch.uint8, device="cuda")
+    assert ws.numel() >= ops.workspace_bytes(T, H, E, K, I)
+    ws.fill_(0xA5)  # the layer must write every byte it reads
+    y_d, ids_d, w_d, eo_d = ops.moe_layer_fused(x_d, wg_d, ew_d, K, workspace=ws)
+    ids, w = host(ids_d), host(w_d)
+    check_routing(ids, w, x, wg, K, f"fused layer T{T} E{E}")
+    if schedule == 1:
+        check_permute(host(ws), ids, E)
+    n = min(T, 48)
+    eo = f32(host(eo_d))
+    within(oracle.compare(eo[:n], oracle.expert_ffn(f32(x[:n]), ids[:n], f32(ew), I)), max_abs=1e-2, mean_abs=1e-3,
+           cos=0.9999)
+    y_o = oracle.combine(eo, f32(w)).astype(np.float16)
+    assert np.array_equal(host(y_d).view(np.uint16), y_o.view(np.uint16))
+    ref = ops.moe_layer(x_d, wg_d, ew_d, K)
+    for name, a, b in zip(("y", "ids", "weights", "expert_out"), ref, (y_d, ids_d, w_d, eo_d)):
+        assert torch.equal(a, b), name
 
 
 def test_decode_uses_streaming_and_prefill_uses_tiled():
