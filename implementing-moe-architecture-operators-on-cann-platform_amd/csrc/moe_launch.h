@@ -7,7 +7,7 @@
 
 namespace moe {
 
-constexpr int kMaxTopK = 32;  // the largest topK the library accepts (phase 2 of routing keeps this many picks)
+constexpr int kRankTopK = 32;  // topK up to which the routing tail ranks its block's slots in one pass
 
 // Per-kernel HIP-event timing (moe_trace.h). A TraceScope brackets exactly one kernel launch.
 class TraceScope {

@@ -47,7 +47,6 @@ moe_status check_routing_sizes(int64_t T, int64_t H, int64_t E, int64_t K) {
     if (K < 1 || K > E) return fail(MOE_ERR_ARG, "topK=%lld must be in [1, numExperts=%lld]", (long long)K, (long long)E);
     if (H % 32 != 0) return fail(MOE_ERR_UNSUPPORTED, "hiddenSize=%lld must be a multiple of 32", (long long)H);
     if (E > kMaxExperts) return fail(MOE_ERR_UNSUPPORTED, "numExperts=%lld exceeds %lld", (long long)E, (long long)kMaxExperts);
-    if (K > moe::kMaxTopK) return fail(MOE_ERR_UNSUPPORTED, "topK=%lld exceeds %lld", (long long)K, (long long)moe::kMaxTopK);
     if (T * H > kInt32Max * 8LL || T * K > kInt32Max)
         return fail(MOE_ERR_UNSUPPORTED, "T=%lld too large", (long long)T);
     return ok();
@@ -76,7 +75,6 @@ moe_status check_combine_sizes(int64_t T, int64_t H, int64_t K) {
         return fail(MOE_ERR_ARG, "sizes must be T >= 0, H > 0, K >= 1 (T=%lld H=%lld K=%lld)", (long long)T,
                     (long long)H, (long long)K);
     if (H % 8 != 0) return fail(MOE_ERR_UNSUPPORTED, "hiddenSize=%lld must be a multiple of 8", (long long)H);
-    if (K > moe::kMaxTopK) return fail(MOE_ERR_UNSUPPORTED, "topK=%lld exceeds %lld", (long long)K, (long long)moe::kMaxTopK);
     if (T * K > kInt32Max) return fail(MOE_ERR_UNSUPPORTED, "T*K too large");
     return ok();
 }

@@ -37,7 +37,7 @@ constexpr int kScatterThreads = 256;  // 4 waves per scatter workgroup (1024 was
 __global__ __launch_bounds__(kThreads) void permute_count_kernel(const int32_t* __restrict__ ids, int S, int E,
                                                                  int32_t* __restrict__ counts,
                                                                  int32_t* __restrict__ rank) {
-    __shared__ int wcnt[(kThreads / kWave) * kMaxE];
+    __shared__ int wcnt[(kThreads / kWave + 1) * kMaxE];
     const int s0 = static_cast<int>(blockIdx.x) * kChunk;
     rank_slots<kThreads / kWave, 4>(ids, s0, min(S, s0 + kChunk), E, counts_stride(E), wcnt,
                                     counts + static_cast<size_t>(blockIdx.x) * counts_stride(E), rank);

@@ -341,7 +341,7 @@ __global__ __launch_bounds__(waves_for(EB, TB) * kWave) void routing_topk_kernel
     // ---- optional tail: the block's slots ranked by expert, for the permute's scatter ----
     if (counts != nullptr) {
         __syncthreads();  // the block's ids are written and part[] is no longer read
-        constexpr int MAXIT = (NT * kMaxTopK + W * kWave - 1) / (W * kWave);
+        constexpr int MAXIT = (NT * kRankTopK + W * kWave - 1) / (W * kWave);
         rank_slots<W, MAXIT>(expert_ids, t0 * K, min(T, t0 + NT) * K, E, counts_stride(E),
                              reinterpret_cast<int*>(part), counts + static_cast<size_t>(blockIdx.x) * counts_stride(E),
                              rank);
@@ -462,7 +462,7 @@ __global__ __launch_bounds__(kWideWaves * kWave) void routing_wide_kernel(const 
     // ---- optional tail: the block's slots ranked by expert, for the permute's scatter ----
     if (counts != nullptr) {
         __syncthreads();  // the block's ids are written and the logits are no longer read
-        constexpr int MAXIT = (kWideTokens * kMaxTopK + kWideWaves * kWave - 1) / (kWideWaves * kWave);
+        constexpr int MAXIT = (kWideTokens * kRankTopK + kWideWaves * kWave - 1) / (kWideWaves * kWave);
         rank_slots<kWideWaves, MAXIT>(expert_ids, t0 * K, min(T, t0 + kWideTokens) * K, E, counts_stride(E),
                                       reinterpret_cast<int*>(logits),
                                       counts + static_cast<size_t>(blockIdx.x) * counts_stride(E), rank);

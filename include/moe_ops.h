@@ -27,7 +27,7 @@
  * references use [H, I], and this library follows the CPU references.
  *
  * Limits of the gfx950 kernels (MOE_ERR_UNSUPPORTED otherwise): H % 32 == 0, I % 32 == 0,
- * 1 <= K <= E <= 256, K <= 32, T*K < 2^31, and 16-byte aligned x, expert_weights, expert_out and y.
+ * 1 <= K <= E <= 256, T*K < 2^31, and 16-byte aligned x, expert_weights, expert_out and y.
  */
 #ifndef MOE_OPS_H
 #define MOE_OPS_H

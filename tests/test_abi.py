@@ -202,6 +202,16 @@ def test_layer_workspace_adds_the_routing_counts_on_the_tiled_schedule(lib):
     assert lib.moe_layer_workspace_bytes(128, 2048, 16, 2, 8200) == 0  # I % 32 != 0
 
 
+def test_top_k_up_to_the_expert_count(lib):
+    rp = lib_mod.RoutingPlan()
+    fp = lib_mod.FfnPlan()
+    for E, K in ((64, 64), (256, 256), (48, 40)):
+        assert lib.moe_routing_topk_plan(1000, 2048, E, K, C.byref(rp)) == MOE_OK, (E, K)
+        assert lib.moe_expert_ffn_plan(1000, 2048, E, K, 1408, C.byref(fp)) == MOE_OK, (E, K)
+        assert lib.moe_layer_workspace_bytes(1000, 2048, E, K, 1408) > 0
+    assert lib.moe_routing_topk_plan(1000, 2048, 64, 65, C.byref(rp)) == ERR_ARG  # K > E
+
+
 def test_last_error_is_cleared_on_success(lib):
     assert _routing_infer(lib, [7, 64], [32, 4], 2)[0] == ERR_SHAPE
     assert lib.moe_last_error() != b""

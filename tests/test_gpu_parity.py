@@ -240,7 +240,9 @@ def test_combine_k1_is_copy_and_equal_weights_mean(ops):
 @pytest.mark.parametrize("T,H,E,K", [(37, 64, 4, 2), (16, 96, 8, 8), (200, 256, 64, 6), (5, 32, 256, 32),
                                      (1, 2048, 16, 2), (33, 128, 1, 1), (1000, 512, 130, 4),
                                      # two and four 16-token blocks per workgroup, T not a multiple of them
-                                     (8200, 64, 20, 3), (16400, 96, 64, 6), (16384, 64, 8, 2)])
+                                     (8200, 64, 20, 3), (16400, 96, 64, 6), (16384, 64, 8, 2),
+                                     # K up to E, as the reference allows (tests/moe_cpu_sim.cpp:224-243)
+                                     (40, 64, 64, 64), (7, 32, 256, 200), (300, 128, 48, 40)])
 def test_routing_shapes(ops, T, H, E, K):
     rng = np.random.default_rng(T * 1000 + E)
     x = rng.standard_normal((T, H)).astype(np.float16)
@@ -725,6 +727,8 @@ def test_layer_on_a_side_stream(ops):
     (9000, 128, 64, 6, 128, 1),    # two 16-token blocks per workgroup, 192 slots per count chunk
     (17000, 128, 13, 2, 128, 1),   # four 16-token blocks; E % 4 != 0 pads the counts rows
     (3000, 128, 130, 4, 128, 1),   # E > 64: the wide routing kernel counts its 64 tokens
+    (300, 128, 48, 40, 128, 1),    # K = 40: a block's 640 slots are ranked in two passes
+    (1000, 128, 100, 64, 128, 1),  # wide kernel, K = 64: 4096 slots per block, two passes
 ])
 def test_fused_layer_matches_oracle_and_operators(ops, T, H, E, K, I, schedule):
     """moe_layer (routing that also ranks its blocks' slots, one scatter launch, the FFN, the combine): ids and
