@@ -169,7 +169,9 @@ hipError_t launch_layer(const uint16_t* x, const uint16_t* w_gate, const uint16_
             return launch_combine(expert_out, weights, y, T, H, K, stream);
         }
         case 0: {
-            const hipError_t err = launch_routing_topk(x, w_gate, ids, weights, T, H, E, K, stream);
+            hipError_t err = prepare_ffn_stream(H, I);  // the FFN kernels' attributes before the first launch
+            if (err != hipSuccess) return err;
+            err = launch_routing_topk(x, w_gate, ids, weights, T, H, E, K, stream);
             if (err != hipSuccess) return err;
             return launch_ffn_combine(x, ids, weights, expert_weights, expert_out, y, ws, T, H, E, K, I, stream);
         }
