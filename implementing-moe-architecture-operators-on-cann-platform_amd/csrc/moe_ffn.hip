@@ -140,10 +140,9 @@ hipError_t launch_ffn_combine(const uint16_t* x, const int32_t* expert_ids, cons
 
 size_t layer_workspace_bytes(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
     size_t bytes = ffn_workspace_bytes(T, H, E, K, I);
+    // counts for the routing blocks of any routing kernel: at most one block per 16 tokens
     if (ffn_schedule(T, H, E, K, I) == 1)
-        bytes += align_up(sizeof(int32_t) * static_cast<size_t>(routing_blocks(static_cast<int>(T), static_cast<int>(E))) *
-                              counts_stride(static_cast<int>(E)),
-                          256);
+        bytes += align_up(sizeof(int32_t) * static_cast<size_t>((T + 15) / 16) * counts_stride(static_cast<int>(E)), 256);
     return bytes;
 }
 
@@ -160,8 +159,9 @@ hipError_t launch_layer(const uint16_t* x, const uint16_t* w_gate, const uint16_
             int32_t* counts = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + ffn_workspace_bytes(T, H, E, K, I));
             err = launch_routing_topk(x, w_gate, ids, weights, T, H, E, K, stream, counts, rank);
             if (err != hipSuccess) return err;
-            const int nblocks = routing_blocks(T, E);
-            err = launch_permute_scatter(ids, T * K, E, H, counts, rank, nblocks, routing_tokens_per_block(T, E) * K,
+            const bool lw = routing_lds_weights(w_gate, H, E);  // the same choice the routing launch makes
+            const int nblocks = routing_blocks(T, H, E, lw);
+            err = launch_permute_scatter(ids, T * K, E, H, counts, rank, nblocks, routing_tokens_per_block(T, H, E, lw) * K,
                                          permute_scatter_chunks_per_block(nblocks), ws, expert_out, stream);
             if (err != hipSuccess) return err;
             err = launch_ffn_tiled(x, expert_weights, expert_out, ws, T, H, E, K, I, stream, /*allow_split=*/true);

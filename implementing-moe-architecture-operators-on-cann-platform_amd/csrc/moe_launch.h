@@ -33,10 +33,12 @@ int resident_workgroups(const void* fn, int threads, size_t lds);
 
 // ---- routing (moe_routing.hip) ----
 int routing_expert_blocks(int E);
-int routing_tokens_per_block(int T, int E);
-int routing_block_threads(int T, int E);
-int routing_lds_bytes(int T, int E);
-int routing_blocks(int T, int E);  // workgroups of a routing launch; each routes routing_tokens_per_block tokens
+// lw: w_gate's rows can reach LDS 16 bytes at a time (E % 8 == 0, 16-byte aligned w_gate): routing_lds_weights
+bool routing_lds_weights(const void* w_gate, int H, int E);
+int routing_tokens_per_block(int T, int H, int E, bool lw);
+int routing_block_threads(int T, int H, int E, bool lw);
+int routing_lds_bytes(int T, int H, int E, bool lw);
+int routing_blocks(int T, int H, int E, bool lw);  // workgroups of a launch, routing_tokens_per_block tokens each
 // counts/rank non-null: the kernel's tail also ranks each block's slots by expert (rank[T*K]) and writes the
 // block's per-expert counts (counts[routing_blocks][counts_stride(E)], 16-byte aligned), the permute's first half
 hipError_t launch_routing_topk(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H,

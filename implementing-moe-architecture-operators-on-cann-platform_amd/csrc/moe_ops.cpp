@@ -142,10 +142,13 @@ moe_status moe_routing_topk_plan(int64_t T, int64_t H, int64_t E, int64_t K, moe
     plan->hidden_size = H;
     plan->num_experts = E;
     plan->top_k = K;
-    plan->tokens_per_block = moe::routing_tokens_per_block(static_cast<int>(T), static_cast<int>(E));
+    // the plan assumes a 16-byte aligned w_gate (hipMalloc memory is); the launch checks the pointer itself
+    const bool lw = E % 8 == 0;
+    plan->tokens_per_block =
+        moe::routing_tokens_per_block(static_cast<int>(T), static_cast<int>(H), static_cast<int>(E), lw);
     plan->grid = static_cast<int32_t>((T + plan->tokens_per_block - 1) / plan->tokens_per_block);
-    plan->block = moe::routing_block_threads(static_cast<int>(T), static_cast<int>(E));
-    plan->lds_bytes = moe::routing_lds_bytes(static_cast<int>(T), static_cast<int>(E));
+    plan->block = moe::routing_block_threads(static_cast<int>(T), static_cast<int>(H), static_cast<int>(E), lw);
+    plan->lds_bytes = moe::routing_lds_bytes(static_cast<int>(T), static_cast<int>(H), static_cast<int>(E), lw);
     plan->workspace_bytes = 0;
     return ok();
 }

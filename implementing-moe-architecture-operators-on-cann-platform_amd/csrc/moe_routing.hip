@@ -3,10 +3,11 @@
 // Reference: op_kernel/moe_routing.cpp (ComputeGate :238-254, SoftmaxRows :263-298, TopKSelect :304-369) and
 // the CPU oracle NaiveMoE steps 1-3, tests/moe_cpu_sim.cpp:198-243.
 //
-// One workgroup owns 16 TB tokens (TB = 1, 2 or 4 blocks of 16, as many as keep >= 256 workgroups); W waves (16
-// when E <= 32, else 4, bounded by the LDS of the partials). Each w_gate fragment a wave loads (8 strided 2-byte
-// loads per lane) is multiplied into all TB token blocks: at T = 16384, E = 64 (TB = 4) that cut the kernel from
-// 80 to 51 us (events), at T = 8192, E = 16 (TB = 2) from 16.6 to 15.2 us.
+// Narrow kernel, E <= 64: one workgroup owns 16 TB tokens (TB = 1, 2 or 4 blocks of 16, as many as keep >= 256
+// workgroups, at most 2 for E > 32); W waves (16 when E <= 32, else 4, bounded by the LDS of the partials). Each
+// w_gate fragment a wave builds is multiplied into all TB token blocks. The fragments come from w_gate rows copied
+// into LDS and read back transposed (E % 8 == 0, 16-byte aligned w_gate), else from 8 strided 2-byte loads per
+// lane; both give the same bits.
 //   Phase 1: logits[16, E] = x[16, H] @ w_gate[H, E] on MFMA (v_mfma_f32_16x16x32_f16, fp32 accumulation;
 //            fp16 x fp16 products are exact in fp32). The H/32 k-steps are dealt round-robin to the W waves; a
 //            wave issues the loads of U k-steps before their MFMAs (at decode, H = 2048 and W = 16: all of a
@@ -17,14 +18,14 @@
 //            runs the softmax, top-K and renormalisation with all-reduces over the row (select_row): max,
 //            expf(l - max), sum, division by the sum; K rounds of an arg-max (lowest index wins an exact tie); the
 //            renormalising sum over the K picks in rank order; fp16 round-to-nearest-even.
-// For E > 64 a wide variant runs instead: a workgroup owns 64 tokens and each of its 4 waves 16 of them over
-// all of H, so no partials are folded. w_gate reaches the waves through LDS: 32-row chunks are read with
-// coalesced loads (one row of E experts is contiguous) and written transposed, [expert][h], so a lane's
-// B fragment (8 consecutive h of one expert) is one ds_read_b128 instead of 8 strided 2-byte global loads.
-// A stage of 2-4 such chunks (64-128 h) is loaded into registers while the previous one is multiplied, two
-// LDS buffers, one barrier per stage. Measured at T = 16384, H = 2048, K = 6: E = 256 takes 206 us here
-// against 425 us in the narrow kernel; at E = 64 the narrow kernel is faster (58 against 62 us: the
-// transposing 2-byte LDS stores cost about what the strided global loads do), so it keeps E <= 64.
+// For E > 64 the rows kernel runs: a workgroup owns 64 tokens and each of its 4 waves 16 of them over all of H,
+// so no partials are folded and the selection runs on the accumulators. w_gate stages (16 KB, row-major) are
+// copied into LDS with 16-byte direct-to-LDS loads and shared by the 4 waves; each wave's x rows stream through its
+// own LDS ring 16 k-steps ahead. T = 16384, H = 2048: E = 256, K = 8 75.7 us; E = 128 42.5 us (the wide kernel
+// below: 171.7 and 95.1 us). When w_gate cannot be copied 16 bytes at a time (E % 8 != 0, unaligned) the wide
+// kernel runs instead: its w_gate chunks are read with coalesced loads and written transposed, [expert][h], so a
+// lane's B fragment is one ds_read_b128; a stage of 2-4 chunks is loaded into registers while the previous one is
+// multiplied, two LDS buffers, one barrier per stage.
 // HBM traffic per launch: T*H*2 (x) + H*E*2 (w_gate, L2-resident after the first workgroups) + T*K*6 bytes.
 
 #include "moe_device.h"
@@ -89,17 +90,18 @@ __device__ __forceinline__ float row_partner(float v) {
 // them in rank order (the oracle's order, tests/moe_cpu_sim.cpp:224-243); lane gl writes picks gl, gl + 16, ...
 // below K. All 64 lanes of the wave must call this (DPP reads the neighbours' registers); only rows with
 // `active` set write.
+// select_vals takes the lane's logits v[q] (expert gl + 16 q) from registers; select_row reads them from an LDS
+// row of the token's logits.
 template <int EPL>
-__device__ __forceinline__ void select_row(const float* row, int E, int K, bool active, int32_t* ids_out,
-                                           uint16_t* w_out) {
+__device__ __forceinline__ void select_vals(float (&v)[EPL], int E, int K, bool active, int32_t* ids_out,
+                                            uint16_t* w_out) {
     constexpr int G = kSelLanes;
     const int gl = lane_id() & (G - 1);
-    float v[EPL];
     float mx = -1e30f;  // the oracle's starting maximum
 #pragma unroll
     for (int q = 0; q < EPL; ++q) {
         const int e = gl + G * q;
-        v[q] = e < E ? row[e] : -1e30f;
+        v[q] = e < E ? v[q] : -1e30f;
         mx = fmaxf(mx, v[q]);
     }
     mx = fmaxf(mx, row_partner<0>(mx));
@@ -169,6 +171,16 @@ __device__ __forceinline__ void select_row(const float* row, int E, int K, bool 
             }
         }
     }
+}
+
+template <int EPL>
+__device__ __forceinline__ void select_row(const float* row, int E, int K, bool active, int32_t* ids_out,
+                                           uint16_t* w_out) {
+    const int gl = lane_id() & (kSelLanes - 1);
+    float v[EPL];
+#pragma unroll
+    for (int q = 0; q < EPL; ++q) v[q] = gl + kSelLanes * q < E ? row[gl + kSelLanes * q] : 0.0f;
+    select_vals<EPL>(v, E, K, active, ids_out, w_out);
 }
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -469,6 +481,152 @@ __global__ __launch_bounds__(kWideWaves * kWave) void routing_wide_kernel(const 
     }
 }
 
+// ---- the rows kernel: each wave owns 16 tokens over all of H, w_gate stages shared by the workgroup ----
+// A workgroup of kRowWaves waves routes kRowTokens tokens. Per stage of SK 32-row k-steps (16 KB of w_gate):
+//   * the four waves copy the stage's w_gate rows, in their own row-major layout (16-byte chunks XOR-swizzled by
+//     row), into a ring of kRowWStages shared LDS stages with 16-byte direct-to-LDS loads, three stages ahead,
+//     one barrier per stage;
+//   * each wave copies its 16 token rows of x (64 B per row and k-step) into its own LDS ring, kRowXDepth k-steps
+//     ahead of their use, so each CU keeps ~64 KB of x in flight without spending registers on it;
+//   * A fragments are ds_read_b128 from the x ring, B fragments two ds_read_b64_tr_b16 from the w_gate stage.
+// The k-steps add in order into one accumulator set. The kernel runs for E > 64 whenever its copies can (E % 8 ==
+// 0, a 16-byte aligned w_gate, SK dividing H / 32), for every T, so a token's bits do not depend on its batch.
+// At E <= 64 it was slower than the narrow kernel (T = 16384, E = 64: 27.8 µs alone and 34.2 µs in the layer,
+// against 21.8 and 30.2 µs): every wave reads all of w_gate from LDS, four times the narrow kernel's share.
+// The selection then runs on the accumulators: the MFMA leaves lane (row kg = lane / 16, column n) with token
+// 4 kg + r, expert 16 b + n in acc[b][r], i.e. each 16-lane DPP row holds one token's experts as select_vals
+// wants them.
+constexpr int kRowWaves = 4;
+constexpr int kRowTokens = 16 * kRowWaves;
+constexpr int kRowXDepth = 16;                                               // x k-steps in flight per wave
+constexpr int kRowWStages = 4;                                               // w_gate ring: 3 stages ahead
+constexpr int row_stage_ksteps(int eb) { return eb >= 16 ? 1 : 16 / eb; }   // 16 KB of w_gate per stage
+constexpr size_t row_lds_bytes(int eb) {
+    return kRowWStages * 16384 + static_cast<size_t>(kRowWaves) * (kRowXDepth + row_stage_ksteps(eb)) * 1024;
+}
+
+template <int EB>
+__global__ __launch_bounds__(kRowWaves * kWave) void routing_rows_kernel(const uint16_t* __restrict__ x,
+                                                                          const uint16_t* __restrict__ w_gate,
+                                                                          int32_t* __restrict__ expert_ids,
+                                                                          uint16_t* __restrict__ weights, int T,
+                                                                          int H, int E, int K,
+                                                                          int32_t* __restrict__ counts,
+                                                                          int32_t* __restrict__ rank) {
+    constexpr int Epad = EB * 16;
+    constexpr int SK = row_stage_ksteps(EB);
+    constexpr int NW = kRowWStages;       // w_gate ring slots; stage i + NW - 1 is copied while i is used
+    constexpr int NXS = kRowXDepth / SK;  // x stages issued ahead of the one in use (>= NW, see the wait below)
+    constexpr int XR = NXS + 1;           // x ring slots (stages) per wave
+    constexpr int kStage = SK * 32 * Epad * 2;
+    static_assert(kStage == 16384 && NXS >= NW && NW >= 2, "stage geometry");
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int lane = lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+    uint8_t* wbuf = lds;                                          // [NW][kStage]
+    uint8_t* xbuf = lds + NW * kStage + wave * XR * SK * 1024;    // this wave's ring: [XR][SK][16 rows][64 B]
+    const int t0 = static_cast<int>(blockIdx.x) * kRowTokens;
+    const int nst = H / 32 / SK;  // the host runs this kernel only when SK divides H / 32
+
+    const __amdgpu_buffer_rsrc_t wrs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(w_gate), 0, H * E * 2, 0x00020000);
+    const __amdgpu_buffer_rsrc_t xrs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(x), 0, T * H * 2, 0x00020000);
+    // x copy: lane -> row lane / 4 (token t0 + 16 wave + row, clamped into the batch), 16-byte chunk lane % 4
+    const int xoff = (min(t0 + wave * 16 + lane / 4, T - 1) * H + (lane % 4) * 8) * 2;
+    // w_gate copy: wave w fills 1 KB slabs w, w + 4, w + 8, w + 12 of a stage; lane -> 16-byte slot of the slab
+    int woff[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const int off = (wave + 4 * m) * 1024 + lane * 16;
+        const int R = off / (32 * EB), pc = (off % (32 * EB)) / 16;  // stage row (SK k-steps of 32), slot
+        const int c = pc ^ ((R % 32) & (2 * EB - 1));                 // the logical chunk stored in slot pc
+        woff[m] = (R * E + (c * 8 < E ? c * 8 : 0)) * 2;              // padding chunks copy any valid chunk
+    }
+    // fragment reads: A at row * 64 + kg * 16 of a k-step's x block; B as in the narrow kernel's LDS path
+    const int arow = lane & 15, kg = lane >> 4;
+    int frag_off[2][EB];
+    {
+        const int sl = lane & 15;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int b = 0; b < EB; ++b) {
+                const int r = 8 * kg + 4 * h + sl / 4;
+                const int e = 16 * b + 4 * (sl % 4);
+                frag_off[h][b] = wstage_chunk<EB>(r, e / 8) + (e % 8) * 2;
+            }
+    }
+    auto issue_w = [&](int st) __attribute__((always_inline)) {
+        uint8_t* dst = wbuf + (st % NW) * kStage;
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (__attribute__((address_space(3))) void*)(dst + (wave + 4 * m) * 1024),
+                                                     16, static_cast<int>(woff[m]), st * SK * 32 * E * 2, 0, 0);
+    };
+    auto issue_x = [&](int st) __attribute__((always_inline)) {
+#pragma unroll
+        for (int ks = 0; ks < SK; ++ks)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (__attribute__((address_space(3))) void*)(xbuf + ((st % XR) * SK + ks) * 1024),
+                                                     16, xoff, (st * SK + ks) * 64, 0, 0);
+    };
+
+    f32x4 acc[EB];
+#pragma unroll
+    for (int b = 0; b < EB; ++b) acc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // Issue order: x(0 .. NXS-1), w(0 .. NW-2), then per iteration j: w(j + NW - 1), x(j + NXS).
+    for (int st = 0; st < min(NXS, nst); ++st) issue_x(st);
+    for (int st = 0; st < min(NW - 1, nst); ++st) issue_w(st);
+    for (int i = 0; i < nst; ++i) {
+        // This wave's copies of w_gate stage i and of x stage i have landed. After w(i) (iteration i - NW + 1, or
+        // the prologue) came x(i - NW + 1 + NXS) and then NW - 2 iterations of w + x: SK + (NW - 2)(4 + SK) copies
+        // when every one of them went out, i.e. when iteration i - 1 still issued both; otherwise wait for all.
+        // x(i) went out no later than iteration i - NXS <= i - NW, before w(i).
+        if (i >= NW - 1 && i + NW - 2 < nst && i - 1 + NXS < nst) {
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(SK + (NW - 2) * (4 + SK)));
+        } else {
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        }
+        __syncthreads();  // every wave's w(i) is visible; every wave is done with w(i - 1) and its x(i - 1)
+        if (i + NW - 1 < nst) issue_w(i + NW - 1);
+        if (i + NXS < nst) issue_x(i + NXS);
+        const uint8_t* ws = wbuf + (i % NW) * kStage;
+        const uint8_t* xs = xbuf + (i % XR) * SK * 1024;
+#pragma unroll
+        for (int ks = 0; ks < SK; ++ks) {
+            const f16x8 a = *reinterpret_cast<const f16x8*>(xs + ks * 1024 + arow * 64 + kg * 16);
+            const uint8_t* wk = ws + ks * 32 * Epad * 2;
+#pragma unroll
+            for (int b = 0; b < EB; ++b) {
+                const s16x4 lo = lds_read_tr16(wk + frag_off[0][b]);
+                const s16x4 hi = lds_read_tr16(wk + frag_off[1][b]);
+                const f16x8 bv = __builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+                acc[b] = mfma16x16x32(a, bv, acc[b]);
+            }
+        }
+    }
+    // ---- selection from the accumulators: round r routes token 4 kg + r of each DPP row ----
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        float v[EB];
+#pragma unroll
+        for (int b = 0; b < EB; ++b) v[b] = acc[b][r];
+        const int t = t0 + wave * 16 + 4 * kg + r;
+        const bool active = t < T;
+        const int tr = active ? t : 0;
+        select_vals<EB>(v, E, K, active, expert_ids + static_cast<size_t>(tr) * K, weights + static_cast<size_t>(tr) * K);
+    }
+    // ---- optional tail: the block's slots ranked by expert, for the permute's scatter ----
+    if (counts != nullptr) {
+        __syncthreads();  // the block's ids are written and the stages are no longer read
+        constexpr int MAXIT = (kRowTokens * kRankTopK + kRowWaves * kWave - 1) / (kRowWaves * kWave);
+        rank_slots<kRowWaves, MAXIT>(expert_ids, t0 * K, min(T, t0 + kRowTokens) * K, E, counts_stride(E),
+                                     reinterpret_cast<int*>(lds),
+                                     counts + static_cast<size_t>(blockIdx.x) * counts_stride(E), rank);
+    }
+}
+
 size_t wide_lds_bytes(int eb) {
     const int pitch = eb == 8 ? wide_pitch(8) : wide_pitch(16);
     return static_cast<size_t>(2) * eb * 16 * pitch * sizeof(uint16_t) +
@@ -520,6 +678,31 @@ hipError_t launch_eb(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, ui
     }
 }
 
+template <int EB>
+hipError_t launch_rows(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H, int E,
+                       int K, int32_t* counts, int32_t* rank, hipStream_t stream) {
+    const int grid = (T + kRowTokens - 1) / kRowTokens;
+    const size_t lds = row_lds_bytes(EB);
+    const hipError_t attr = ensure_lds_limit(reinterpret_cast<const void*>(&routing_rows_kernel<EB>),
+                                             static_cast<int>(lds));
+    if (attr != hipSuccess) return attr;
+    TraceScope trace("moe_routing_topk", stream);
+    routing_rows_kernel<EB><<<grid, kRowWaves * kWave, lds, stream>>>(x, w_gate, ids, w, T, H, E, K, counts, rank);
+    return hipGetLastError();
+}
+
+// Which kernel routes: the narrow kernel for E <= 64; for E > 64 the rows kernel when its copies can run (lw:
+// w_gate rows can be copied 16 bytes at a time; x within 32-bit buffer offsets), else the wide kernel. The choice
+// does not depend on T.
+enum RoutingKernel { kNarrowKernel, kWideKernel, kRowsKernel };
+RoutingKernel routing_kernel(int T, int H, int E, bool lw) {
+    const int eb = routing_expert_blocks(E);
+    if (eb <= 4) return kNarrowKernel;
+    const bool rows_ok = lw && (H / 32) % row_stage_ksteps(eb) == 0 &&
+                         static_cast<int64_t>(T) * H * 2 < (int64_t{1} << 31);
+    return rows_ok ? kRowsKernel : kWideKernel;
+}
+
 }  // namespace
 
 int routing_expert_blocks(int E) {
@@ -531,27 +714,45 @@ int routing_expert_blocks(int E) {
     return 16;
 }
 
-int routing_tokens_per_block(int T, int E) {
-    return routing_expert_blocks(E) <= 4 ? kTokensPerBlock * narrow_token_blocks(T, routing_expert_blocks(E)) : kWideTokens;
-}
-int routing_block_threads(int T, int E) {
-    const int eb = routing_expert_blocks(E);
-    return eb <= 4 ? waves_for(eb, narrow_token_blocks(T, eb)) * kWave : kWideWaves * kWave;
-}
-int routing_lds_bytes(int T, int E) {
-    const int eb = routing_expert_blocks(E);
-    if (eb > 4) return static_cast<int>(wide_lds_bytes(eb));
-    return static_cast<int>(narrow_lds_bytes(eb, narrow_token_blocks(T, eb), E % 8 == 0));
-}
+bool routing_lds_weights(const void* w_gate, int H, int E) { return narrow_lds_weights(w_gate, H, E); }
 
-int routing_blocks(int T, int E) {
-    const int tpb = routing_tokens_per_block(T, E);
+int routing_tokens_per_block(int T, int H, int E, bool lw) {
+    const int eb = routing_expert_blocks(E);
+    switch (routing_kernel(T, H, E, lw)) {
+        case kRowsKernel: return kRowTokens;
+        case kWideKernel: return kWideTokens;
+        default: return kTokensPerBlock * narrow_token_blocks(T, eb);
+    }
+}
+int routing_block_threads(int T, int H, int E, bool lw) {
+    const int eb = routing_expert_blocks(E);
+    switch (routing_kernel(T, H, E, lw)) {
+        case kRowsKernel: return kRowWaves * kWave;
+        case kWideKernel: return kWideWaves * kWave;
+        default: return waves_for(eb, narrow_token_blocks(T, eb)) * kWave;
+    }
+}
+int routing_lds_bytes(int T, int H, int E, bool lw) {
+    const int eb = routing_expert_blocks(E);
+    switch (routing_kernel(T, H, E, lw)) {
+        case kRowsKernel: return static_cast<int>(row_lds_bytes(eb));
+        case kWideKernel: return static_cast<int>(wide_lds_bytes(eb));
+        default: return static_cast<int>(narrow_lds_bytes(eb, narrow_token_blocks(T, eb), lw));
+    }
+}
+int routing_blocks(int T, int H, int E, bool lw) {
+    const int tpb = routing_tokens_per_block(T, H, E, lw);
     return (T + tpb - 1) / tpb;
 }
 
 hipError_t launch_routing_topk(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H,
                                int E, int K, hipStream_t stream, int32_t* counts, int32_t* rank) {
-    switch (routing_expert_blocks(E)) {
+    const int eb = routing_expert_blocks(E);
+    if (routing_kernel(T, H, E, narrow_lds_weights(w_gate, H, E)) == kRowsKernel) {
+        return eb == 8 ? launch_rows<8>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream)
+                       : launch_rows<16>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);
+    }
+    switch (eb) {
         case 1: return launch_eb<1>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);
         case 2: return launch_eb<2>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);
         case 4: return launch_eb<4>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);

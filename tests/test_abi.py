@@ -107,8 +107,13 @@ def test_plans(lib):
     assert (rp.grid, rp.block, rp.tokens_per_block, rp.lds_bytes) == (512, 256, 32, 4 * (32 * 64 * 4 + 2 * 32 * 64 * 2))
     assert lib.moe_routing_topk_plan(8192, 2048, 16, 2, C.byref(rp)) == MOE_OK
     assert (rp.grid, rp.block, rp.tokens_per_block, rp.lds_bytes) == (256, 1024, 32, 16 * (32 * 16 * 4 + 4 * 32 * 16 * 2))
-    # E > 64: the wide kernel, 64 tokens per workgroup, w_gate via LDS
+    # E > 64: 64 tokens per workgroup; the rows kernel (4 waves of 16 tokens over all of H, four 16 KB w_gate
+    # stages, each wave's x ring of 16 + 1 k-steps of 1 KB)
     assert lib.moe_routing_topk_plan(16384, 2048, 256, 8, C.byref(rp)) == MOE_OK
+    assert (rp.grid, rp.block, rp.tokens_per_block) == (256, 256, 64)
+    assert rp.lds_bytes == 4 * 16384 + 4 * (16 + 1) * 1024  # the rows kernel: 4 w_gate stages, x rings
+    # E % 8 != 0 (no 16-byte w_gate rows): the wide kernel, w_gate transposed through LDS
+    assert lib.moe_routing_topk_plan(16384, 2048, 250, 8, C.byref(rp)) == MOE_OK
     assert (rp.grid, rp.block, rp.tokens_per_block) == (256, 256, 64)
     assert rp.lds_bytes == 2 * 256 * (2 * 32 + 8) * 2 + 64 * 256 * 4  # 2 stages of 64 h, fp32 logits
     assert lib.moe_routing_topk_plan(128, 2040, 16, 2, C.byref(rp)) == ERR_UNSUP
@@ -194,10 +199,11 @@ def test_launch_argument_errors_return_before_launch(lib):
 def test_layer_workspace_adds_the_routing_counts_on_the_tiled_schedule(lib):
     # streaming schedule (decode): the FFN's workspace as it is
     assert lib.moe_layer_workspace_bytes(128, 2048, 16, 2, 8192) == lib.moe_expert_ffn_workspace_bytes(128, 2048, 16, 2, 8192)
-    # tiled schedule: + one row of counts_stride(E) int32 per routing workgroup, 256-byte aligned
-    for T, E, blocks in ((16384, 64, 512), (8192, 16, 256), (3000, 130, 47)):
+    # tiled schedule: + one row of counts_stride(E) int32 per 16 tokens (the most routing workgroups any routing
+    # kernel runs), 256-byte aligned
+    for T, E in ((16384, 64), (8192, 16), (3000, 130), (3001, 13)):
         ffn = lib.moe_expert_ffn_workspace_bytes(T, 2048, E, 6, 1408)
-        extra = (blocks * ((E + 3) // 4 * 4) * 4 + 255) // 256 * 256
+        extra = ((T + 15) // 16 * ((E + 3) // 4 * 4) * 4 + 255) // 256 * 256
         assert lib.moe_layer_workspace_bytes(T, 2048, E, 6, 1408) == ffn + extra, (T, E)
     assert lib.moe_layer_workspace_bytes(128, 2048, 16, 2, 8200) == 0  # I % 32 != 0
 

@@ -251,10 +251,11 @@ def test_routing_shapes(ops, T, H, E, K):
     check_routing(host(ids_d), host(w_d), x, wg, K, f"routing T{T} H{H} E{E} K{K}")
 
 
-@pytest.mark.parametrize("E,K", [(16, 2), (64, 6)])
+@pytest.mark.parametrize("E,K", [(16, 2), (64, 6), (40, 5)])
 def test_routing_is_batch_invariant(ops, E, K):
-    """A token's ids and weights do not depend on the batch it is routed in: 16400 tokens run 4 token blocks per
-    workgroup, their first 1000 alone run 1, and the rows agree bit for bit."""
+    """A token's ids and weights do not depend on the batch it is routed in: 16400 tokens run several token
+    blocks per workgroup (E <= 32) or the rows kernel (32 < E <= 64), their first 1000 alone run the narrow
+    kernel with one block, and the rows agree bit for bit."""
     T, H = 16400, 512
     rng = np.random.default_rng(E)
     x = rng.standard_normal((T, H)).astype(np.float16)
@@ -263,6 +264,29 @@ def test_routing_is_batch_invariant(ops, E, K):
     ids_few, w_few = ops.MoeRoutingTopK(dev(x[:1000]), dev(wg), K)
     assert np.array_equal(host(ids_all)[:1000], host(ids_few))
     assert np.array_equal(host(w_all)[:1000].view(np.uint16), host(w_few).view(np.uint16))
+
+
+@pytest.mark.parametrize("T,H,E,K", [(9000, 256, 64, 6), (8192, 128, 48, 8), (20000, 2048, 64, 6),
+                                     (3000, 256, 72, 6), (2100, 64, 256, 8), (70, 128, 200, 40)])
+def test_routing_lds_weight_paths(ops, T, H, E, K):
+    """w_gate through LDS: the narrow kernel's transposing-read path (E <= 64) and the rows kernel (E > 64, each
+    wave 16 tokens over all of H). ids and weights against the oracle on every token; for E <= 64 also bit for bit
+    against the 2-byte gathers, which run when w_gate is not 16-byte aligned (the same values one fp16 further
+    into a larger buffer)."""
+    log(f"[lds w_gate] T={T} H={H} E={E} K={K}")
+    rng = np.random.default_rng(T + E)
+    x = rng.standard_normal((T, H)).astype(np.float16)
+    wg = (rng.standard_normal((H, E)) / math.sqrt(H)).astype(np.float16)
+    ids_d, w_d = ops.MoeRoutingTopK(dev(x), dev(wg), K)
+    ids, w = host(ids_d), host(w_d)
+    check_routing(ids, w, x, wg, K, f"rows T{T} H{H} E{E} K{K}")
+    if E <= 64:
+        buf = torch.empty(H * E + 8, dtype=torch.float16, device="cuda")
+        wg_odd = buf[1: 1 + H * E].view(H, E)  # 2-byte aligned only: the narrow kernel's 2-byte gathers
+        wg_odd.copy_(dev(wg))
+        ids2, w2 = ops.MoeRoutingTopK(dev(x), wg_odd, K)
+        assert np.array_equal(ids, host(ids2))
+        assert np.array_equal(w.view(np.uint16), host(w2).view(np.uint16))
 
 
 def test_routing_exact_ties_lowest_index_first(ops):
