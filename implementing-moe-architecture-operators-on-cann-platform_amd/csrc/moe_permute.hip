@@ -64,7 +64,7 @@ __global__ __launch_bounds__(kScatterThreads) void permute_scatter_kernel(
 #pragma unroll
         for (int u = 0; u < kBatch; ++u) {
             const int s = sb + u * kScatterThreads;
-            e[u] = s < s_end ? ids[s] : -2;
+            e[u] = s < s_end ? ids[s] : 0;
             r[u] = s < s_end ? rank[s] : 0;
         }
     };
@@ -154,9 +154,10 @@ __global__ __launch_bounds__(kScatterThreads) void permute_scatter_kernel(
 #pragma unroll
         for (int u = 0; u < kBatch; ++u) {
             const int s = sb + u * kScatterThreads;
+            if (s >= s_end) continue;
             if (e[u] >= 0 && e[u] < E) {
                 sorted_slot[lbase[(s / chunk_slots - c0) * E + e[u]] + r[u]] = s;
-            } else if (e[u] != -2) {  // belongs to no expert: its expert_out row is zero
+            } else {  // belongs to no expert: its expert_out row is zero
                 u32x4* row = reinterpret_cast<u32x4*>(expert_out + static_cast<size_t>(s) * H);
                 for (int jj = 0; jj < H / 8; ++jj) row[jj] = u32x4{0u, 0u, 0u, 0u};
             }

@@ -634,6 +634,38 @@ def test_ffn_tiled_unaligned_expert_ids(ops):
     assert np.array_equal(host(eo_u).view(np.uint16), host(eo_a).view(np.uint16))
 
 
+def test_ffn_tiled_invalid_ids_give_zero_rows(ops):
+    """Tiled schedule, ids outside [0, E) of every kind (-2, -1, E, a large value): those expert_out rows are zero
+    (written over a non-zero buffer), they take no place in the permutation, and every other row matches the
+    oracle."""
+    T, H, E, K, I = 600, 128, 8, 3, 128
+    assert ffn_schedule(T, H, E, K, I) == 1
+    rng = np.random.default_rng(37)
+    x = rng.standard_normal((T, H)).astype(np.float16)
+    ew = np.concatenate([rng.standard_normal((E, 2 * I, H)) / math.sqrt(H),
+                         rng.standard_normal((E, I, H)) / math.sqrt(I)], axis=1).astype(np.float16)
+    ids = np.stack([rng.permutation(E)[:K] for _ in range(T)]).astype(np.int32)
+    bad = rng.choice(T * K, 40, replace=False)
+    ids.ravel()[bad] = np.resize(np.array([-2, -1, E, 1 << 20], np.int32), bad.size)
+    w = np.full((T, K), 1.0 / K, np.float16)
+    x_d, w_d, ew_d = dev(x), dev(w), dev(ew)
+    ws = torch.empty(ops.workspace_bytes(T, H, E, K, I), dtype=torch.uint8, device="cuda")
+    eo_d = torch.full((T, K, H), 7.0, dtype=torch.float16, device="cuda")
+    st = ops._lib.load().moe_expert_ffn(x_d.data_ptr(), dev(ids).data_ptr(), w_d.data_ptr(), ew_d.data_ptr(),
+                                        eo_d.data_ptr(), ws.data_ptr(), ws.numel(), T, H, E, K, I,
+                                        torch.cuda.current_stream().cuda_stream)
+    assert st == 0
+    torch.cuda.synchronize()
+    eo = f32(host(eo_d)).reshape(T * K, H)
+    assert not eo[bad].any()
+    check_permute(host(ws), ids, E)
+    good = np.setdiff1d(np.arange(T * K), bad)
+    ids_valid = ids.copy()
+    ids_valid.ravel()[bad] = 0  # the oracle takes valid ids only; each row depends on its own id alone
+    eo_o = oracle.expert_ffn(f32(x), ids_valid, f32(ew), I).reshape(T * K, H)
+    within(oracle.compare(eo[good], eo_o[good]), max_abs=1e-2, mean_abs=1e-3, cos=0.9999)
+
+
 def test_ffn_tiled_several_tiles_per_workgroup(ops):
     """512 gate/up tiles on a grid of at most one workgroup per CU: each workgroup runs several tiles with the
     copy ring running on from one tile into the next (other experts, other n-tiles). Checked against the oracle
