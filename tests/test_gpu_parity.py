@@ -220,6 +220,53 @@ def test_layer_graph_replay_matches_eager(ops, T, H, E, K, I, schedule):
     del g
 
 
+@pytest.mark.parametrize("T,H,E,K,I,schedule", [(64, 256, 8, 2, 512, 0), (1000, 128, 16, 2, 128, 1)])
+def test_fused_layer_graph_replay(ops, T, H, E, K, I, schedule):
+    """moe_layer (routing with the slot-ranking tail, one scatter launch, the FFN, the combine) captured in a HIP
+    graph: every replay, after eager work that changes x and clears the outputs and the workspace, equals an eager
+    moe_layer bit for bit, and its y is the oracle combine of its expert_out."""
+    lib = ops._lib.load()
+    log(f"[graph moe_layer] T={T} H={H} E={E} K={K} I={I} schedule={schedule}")
+    assert ffn_schedule(T, H, E, K, I) == schedule
+    gen = torch.Generator(device="cpu").manual_seed(T * 3 + I)
+    x = torch.randn(T, H, generator=gen).half().cuda()
+    wg = (torch.randn(H, E, generator=gen) / math.sqrt(H)).half().cuda()
+    ew = (torch.randn(E, 3 * I, H, generator=gen) / math.sqrt(H)).half().cuda()
+    ws_bytes = ops.layer_workspace_bytes(T, H, E, K, I)
+
+    def buffers():
+        return dict(ids=torch.empty(T, K, dtype=torch.int32, device="cuda"),
+                    w=torch.empty(T, K, dtype=torch.float16, device="cuda"),
+                    eo=torch.empty(T, K, H, dtype=torch.float16, device="cuda"),
+                    y=torch.empty(T, H, dtype=torch.float16, device="cuda"),
+                    ws=torch.empty(ws_bytes, dtype=torch.uint8, device="cuda"))
+
+    def step(b, s):
+        st = lib.moe_layer(x.data_ptr(), wg.data_ptr(), ew.data_ptr(), b["ids"].data_ptr(), b["w"].data_ptr(),
+                           b["eo"].data_ptr(), b["y"].data_ptr(), b["ws"].data_ptr(), ws_bytes, T, H, E, K, I, s)
+        assert st == 0, lib.moe_last_error()
+
+    gb, eb = buffers(), buffers()
+    step(gb, torch.cuda.current_stream().cuda_stream)  # first launches set the kernels' LDS attributes
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step(gb, torch.cuda.current_stream().cuda_stream)
+    for i in range(3):
+        x.copy_(torch.randn(T, H, generator=gen).half())
+        step(eb, torch.cuda.current_stream().cuda_stream)
+        for t in gb.values():
+            t.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for name in ("ids", "w", "eo", "y"):
+            assert torch.equal(gb[name], eb[name]), (i, name)
+        y_o = oracle.combine(f32(host(gb["eo"])), f32(host(gb["w"]))).astype(np.float16)
+        assert np.array_equal(host(gb["y"]).view(np.uint16), y_o.view(np.uint16)), i
+    del g
+
+
 def test_combine_bit_exact_random(ops):
     rng = np.random.default_rng(0)
     for T, H, K in ((1, 8, 1), (37, 64, 2), (300, 2048, 6), (5, 4096, 32)):
