@@ -601,6 +601,32 @@ def tiled_down_grid(cfg) -> int:
     return plan.down_grid
 
 
+def test_deepseek_v3_layer_shape_sampled(ops):
+    """The DeepSeek-V3 layer's expert shape (H = 7168, E = 256, K = 8, I = 2048; 22.5 GB of fp16 expert
+    weights) through moe_layer on 2048 Zipf-routed tokens: routing on every token against the oracle, expert_out
+    against the oracle on six tokens (the oracle gets only their experts' weights), y bit for bit the combine of
+    expert_out, and the three operators' run bit for bit."""
+    cfg = synth.MoeConfig(2048, 7168, 256, 8, 2048, zipf=True, name="deepseek_v3_shape")
+    log(f"[{cfg.name}] T={cfg.T} H={cfg.H} E={cfg.E} K={cfg.K} I={cfg.I}: generating inputs on the GPU")
+    x_d, wg_d, ew_d = gpu_inputs(ops, cfg, 45)
+    y_d, ids_d, w_d, eo_d = ops.moe_layer_fused(x_d, wg_d, ew_d, cfg.K)
+    x, wg = host(x_d), host(wg_d)
+    ids, w = host(ids_d), host(w_d)
+    check_routing(ids, w, x, wg, cfg.K, cfg.name)
+    sample = np.linspace(0, cfg.T - 1, 6).astype(np.int64)
+    used = np.unique(ids[sample])  # the sampled tokens' experts, renumbered 0.. for the oracle
+    ids_sub = np.searchsorted(used, ids[sample]).astype(np.int32)
+    ew_sub = f32(host(ew_d[torch.from_numpy(used).cuda()]))
+    eo_o = oracle.expert_ffn(f32(x[sample]), ids_sub, ew_sub, cfg.I)
+    log(f"[{cfg.name}] oracle sample: {len(sample)} tokens, {len(used)} experts")
+    within(oracle.compare(f32(host(eo_d))[sample], eo_o), max_abs=1e-2, mean_abs=1e-3, cos=0.9999)
+    y_o = oracle.combine(f32(host(eo_d)), f32(w)).astype(np.float16)
+    assert np.array_equal(host(y_d).view(np.uint16), y_o.view(np.uint16))
+    ref = ops.moe_layer(x_d, wg_d, ew_d, cfg.K)
+    for name, a, b in zip(("y", "ids", "weights", "expert_out"), ref, (y_d, ids_d, w_d, eo_d)):
+        assert torch.equal(a, b), name
+
+
 def test_reference_target_case_seed44(ops):
     """The reference's own target-size RunTest case (tests/moe_cpu_sim.cpp:862-864: T=128, H=2048, E=16, K=2,
     I=8192, seed 44) on its own generator's inputs rounded to fp16: ids bit-exact against the reference's
