@@ -54,6 +54,13 @@ constexpr int kThreads = 512;      // 8 waves
 constexpr int kStageHalfs = (kBM + kBN) * kPitch;
 constexpr int kNStage = 2;
 constexpr int kLdsBytes = kNStage * kStageHalfs * 2;  // the ring; the tile table follows it
+constexpr int kEpiStageBytes = kThreads / kWave * 2048;  // down epilogue: 16 rows x 128 B per wave
+// LDS of a launch: the ring, the tile table (tab, offs: 2 (E + 1) ints), three row tables, then (down) the
+// epilogue's staging rows at the next 16-byte boundary
+__host__ __device__ constexpr int tiled_epi_stage_offset(int E) { return (kLdsBytes + 8 * (E + 1) + 3 * kBM * 4 + 15) / 16 * 16; }
+__host__ __device__ constexpr int tiled_lds_bytes(int E, bool down) {
+    return down ? tiled_epi_stage_offset(E) + kEpiStageBytes : kLdsBytes + 8 * (E + 1) + 3 * kBM * 4;
+}
 constexpr int kLdsMax = 160 * 1024;
 constexpr int kXcds = 8;
 constexpr int kCopyPolicy = 1;  // cache-policy bits of the stage copies: sc0
@@ -61,6 +68,10 @@ constexpr int kCopyPolicy = 1;  // cache-policy bits of the stage copies: sc0
 constexpr int kMaxParts = 256;
 constexpr int kFixThreads = 256;
 constexpr int kFixRows = 16;  // tile rows per fix-up workgroup
+// The split pays off only while the leftover round is a large share of the down projection: at DeepSeek-V2-Lite
+// prefill (T = 16384, E = 64, K = 6, 13-14 rounds of 22-stage tiles) the unsplit kernel takes 651 us against
+// 677 us + a 17 us fix-up split; at 2-2.5 rounds (T = 8192, E = 16; Mixtral T = 4096) the split saves 100-215 us.
+constexpr int kSplitMaxRounds = 4;
 
 enum Epilogue { kSwiGLU = 0, kScatter = 1 };
 
@@ -424,17 +435,36 @@ __global__ __launch_bounds__(kThreads) void ffn_tiled_kernel(TiledArgs p) {
                 }
             }
         } else {
+            // Whole-line stores: the wave's 128 x 64 sub-tile leaves as 16 instructions of 8 rows x 128 B. Row
+            // block i passes through the wave's own 2 KB of LDS (16 rows x 128 B; 16-byte granule g of row r at
+            // g ^ (r & 7)): lane (row16, kg) writes its four packed 4-column groups, then lane L reads granule
+            // L % 8 of row h * 8 + L / 8 (h = 0, 1). Stored straight from the MFMA layout (16 rows x 32 B per
+            // instruction) the epilogue cost ~100 us per DeepSeek-V2-Lite down launch (T = 16384, E = 64, K = 6).
+            uint8_t* stg = reinterpret_cast<uint8_t*>(lds) + tiled_epi_stage_offset(p.E) + wave * 2048;
+            const int rr = lane >> 3, gq = lane & 7;
+            const int col = cur.nt * kBN + wn * 64 + gq * 8;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                if (m + i * 16 >= cur.ne) continue;
-                uint16_t* dst = p.out + static_cast<size_t>(rowtab[(k % 3) * kBM + wm * 128 + i * 16 + row16]) * p.H;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const int col = cur.nt * kBN + wn * 64 + j * 16 + kg * 4;
-                    if (col >= p.H) continue;
                     const uint32_t lo = f32_to_f16_bits(acc[i][j][0]) | (static_cast<uint32_t>(f32_to_f16_bits(acc[i][j][1])) << 16);
                     const uint32_t hi = f32_to_f16_bits(acc[i][j][2]) | (static_cast<uint32_t>(f32_to_f16_bits(acc[i][j][3])) << 16);
-                    *reinterpret_cast<uint2*>(dst + col) = make_uint2(lo, hi);
+                    *reinterpret_cast<uint2*>(stg + row16 * 128 + (((2 * j + (kg >> 1)) ^ (row16 & 7)) << 4) + ((kg & 1) << 3)) =
+                        make_uint2(lo, hi);
+                }
+                // the reads take what other lanes of this wave just wrote (LDS operations of one wave run in order)
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                u32x4 v[2];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) v[h] = *reinterpret_cast<const u32x4*>(stg + (h * 8 + rr) * 128 + ((gq ^ rr) << 4));
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // read before the next block's writes
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int r = wm * 128 + i * 16 + h * 8 + rr;  // row of the tile
+                    if (cur.mt * kBM + r >= cur.ne || col >= p.H) continue;
+                    *reinterpret_cast<u32x4*>(p.out + static_cast<size_t>(rowtab[(k % 3) * kBM + r]) * p.H + col) = v[h];
                 }
             }
         }
@@ -521,7 +551,7 @@ __global__ __launch_bounds__(kFixThreads) void ffn_tiled_fixup_kernel(TiledArgs 
 template <int EPI, bool SPLIT>
 hipError_t launch_tiled(TiledArgs p, int grid, const char* name, hipStream_t stream) {
     const void* fn = reinterpret_cast<const void*>(&ffn_tiled_kernel<EPI, SPLIT>);
-    const int lds = kLdsBytes + 8 * (p.E + 1) + 3 * kBM * 4;
+    const int lds = tiled_lds_bytes(p.E, EPI == kScatter);
     const int resident = resident_workgroups(fn, kThreads, lds);
     if (resident > 0 && resident < grid) grid = resident;
     grid = grid / kXcds * kXcds;
@@ -548,7 +578,7 @@ hipError_t launch_tiled(TiledArgs p, int grid, const char* name, hipStream_t str
 // over by the ring.
 bool tiled_shape_supported(int64_t H, int64_t E, int64_t I) {
     if (H % kBK != 0 || I % kBK != 0 || H < 2 * kBK || I < 2 * kBK) return false;
-    return kLdsBytes + 8 * (E + 1) + 3 * kBM * 4 <= kLdsMax;
+    return tiled_lds_bytes(static_cast<int>(E), true) <= kLdsMax;
 }
 // The buffer offsets are 32-bit: gathered x rows (T*H*2 bytes), one expert's weights (3*I*H*2) and the sorted
 // slots (T*K*4) must stay below 2 GiB. The down projection addresses hidden per tile, so T*K*I has no such bound.
@@ -560,17 +590,25 @@ bool tiled_supported(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
     return tiled_shape_supported(H, E, I) && tiled_size_supported(T, H, K, I);
 }
 hipError_t prepare_ffn_tiled() {
-    hipError_t err = ensure_lds_limit(reinterpret_cast<const void*>(&ffn_tiled_kernel<kSwiGLU, false>), kLdsMax);
-    if (err != hipSuccess) return err;
-    return ensure_lds_limit(reinterpret_cast<const void*>(&ffn_tiled_kernel<kScatter, true>), kLdsMax);
+    for (const void* fn : {reinterpret_cast<const void*>(&ffn_tiled_kernel<kSwiGLU, false>),
+                           reinterpret_cast<const void*>(&ffn_tiled_kernel<kScatter, false>),
+                           reinterpret_cast<const void*>(&ffn_tiled_kernel<kScatter, true>)}) {
+        const hipError_t err = ensure_lds_limit(fn, kLdsMax);
+        if (err != hipSuccess) return err;
+    }
+    return hipSuccess;
 }
 int tiled_block_threads() { return kThreads; }
-// The down projection splits leftover tiles into pieces of at least two k-stages (so only when I / kBK >= 4); a
-// piece writes the partial slot of its workgroup, and the launch has at most min(kMaxParts, tiled_down_grid)
-// workgroups.
-bool tiled_down_splits(int I) { return I / kBK >= 4; }
+// The down projection splits leftover tiles into pieces of at least two k-stages (so only when I / kBK >= 4), and
+// only when its tiles (bounded by tiled_down_grid) fill at most kSplitMaxRounds rounds of kMaxParts workgroups
+// (one per CU on MI355X); a piece writes the partial slot of its workgroup, and the launch has at most
+// min(kMaxParts, tiled_down_grid) workgroups.
+bool tiled_down_splits(int T, int E, int K, int H, int I) {
+    const int rounds = (tiled_down_grid(T, E, K, H) + kMaxParts - 1) / kMaxParts;
+    return I / kBK >= 4 && rounds <= kSplitMaxRounds;
+}
 size_t tiled_partial_bytes(int T, int H, int E, int K, int I) {
-    if (!tiled_down_splits(I)) return 0;
+    if (!tiled_down_splits(T, E, K, H, I)) return 0;
     const int slots = min(kMaxParts, tiled_down_grid(T, E, K, H));
     return static_cast<size_t>(slots) * kBM * kBN * sizeof(float);
 }
@@ -613,8 +651,9 @@ hipError_t launch_ffn_tiled(const uint16_t* x, const uint16_t* expert_weights, u
     p.ndim = H;
     p.ntiles_n = (H + kBN - 1) / kBN;
     p.gather = 0;
-    p.split = (allow_split && tiled_down_splits(I) && ws.partial != nullptr) ? 1 : 0;
-    return launch_tiled<kScatter, true>(p, tiled_down_grid(T, E, K, H), "moe_ffn_down", stream);
+    p.split = (allow_split && tiled_down_splits(T, E, K, H, I) && ws.partial != nullptr) ? 1 : 0;
+    if (p.split) return launch_tiled<kScatter, true>(p, tiled_down_grid(T, E, K, H), "moe_ffn_down", stream);
+    return launch_tiled<kScatter, false>(p, tiled_down_grid(T, E, K, H), "moe_ffn_down", stream);
 }
 
 }  // namespace moe
