@@ -5,14 +5,14 @@
 //
 // Narrow kernel, E <= 64: one workgroup owns 16 TB tokens (TB = 1, 2 or 4 blocks of 16, as many as keep >= 256
 // workgroups, at most 2 for E > 32); W waves (16 when E <= 32, else 4, bounded by the LDS of the partials). Each
-// w_gate fragment a wave builds is multiplied into all TB token blocks. The fragments come from w_gate rows copied
-// into LDS and read back transposed (E % 8 == 0, 16-byte aligned w_gate), else from 8 strided 2-byte loads per
+// w_gate fragment a wave builds is multiplied into all TB token blocks. The fragments come from w_gate rows staged
+// in LDS and read back transposed (E % 8 == 0, 16-byte aligned w_gate), else from 8 strided 2-byte loads per
 // lane; both give the same bits.
 //   Phase 1: logits[16, E] = x[16, H] @ w_gate[H, E] on MFMA (v_mfma_f32_16x16x32_f16, fp32 accumulation;
-//            fp16 x fp16 products are exact in fp32). The H/32 k-steps are dealt round-robin to the W waves; a
-//            wave issues the loads of U k-steps before their MFMAs (at decode, H = 2048 and W = 16: all of a
-//            wave's loads in one round trip), keeps partial logits of every expert block in registers and parks
-//            them in LDS.
+//            fp16 x fp16 products are exact in fp32). The H/32 k-steps are dealt round-robin to the W waves; with
+//            w_gate through LDS a wave keeps the loads of the next 2-3 k-steps in flight in register rings (at
+//            decode, H = 2048 and W = 16: 4 k-steps a wave), else it issues the loads of U k-steps per round trip;
+//            it keeps partial logits of every expert block in registers and parks them in LDS.
 //   Fold:    one thread per (token, expert) adds the W partials in wave order.
 //   Phase 2: one 16-lane DPP row per token (each lane holding Epad / 16 experts; four tokens per wave at a time)
 //            runs the softmax, top-K and renormalisation with all-reduces over the row (select_row): max,
@@ -57,10 +57,13 @@ int narrow_token_blocks(int T, int eb) {
     const int tb = T >= 16 * 4 * 256 ? 4 : T >= 16 * 2 * 256 ? 2 : 1;
     return eb == 4 ? min(tb, 2) : tb;
 }
-// partial logits, then (lw) every wave's U w_gate stages of 32 rows
+// LW: k-steps per round trip, (TB + EB) * 4 VGPRs of loads each, within the 128 (1024 threads) or 256 (256
+// threads) a lane has
+constexpr int lw_unroll(int eb, int tb) { return eb == 2 && tb == 4 ? 2 : 4; }
+// partial logits, then (lw) every wave's w_gate stage of 32 rows
 constexpr size_t narrow_lds_bytes(int eb, int tb, bool lw) {
     return static_cast<size_t>(waves_for(eb, tb)) * 16 * eb *
-           (tb * 16 * sizeof(float) + (lw ? unroll_for(eb, tb) * 32 * sizeof(uint16_t) : 0));
+           (tb * 16 * sizeof(float) + (lw ? 32 * sizeof(uint16_t) : 0));
 }
 // the LDS path for w_gate: whole 16-byte chunks per row, an aligned base, 32-bit buffer offsets
 bool narrow_lds_weights(const void* w_gate, int H, int E) {
@@ -199,10 +202,11 @@ __device__ __forceinline__ int wstage_chunk(int r, int c) {
 
 // EB = number of 16-expert blocks held in registers (ceil(E / 16) rounded up to an instantiated size); TB = 16-token
 // blocks per workgroup (every w_gate fragment a wave loads is multiplied into all TB of them). LW: w_gate rows
-// reach the wave through LDS (E % 8 == 0 and a 16-byte aligned w_gate): each k-step's 32 rows are copied with
-// 16-byte direct-to-LDS loads in their own row-major layout and the B fragments (8 consecutive h of one expert)
-// come out of ds_read_tr16_b64, which hands lane i of each 16-lane group element i % 4 of the 4-element rows
-// addressed by lanes 4 j + i / 4 (j < 4). Without LW every fragment is 8 strided 2-byte global loads.
+// reach the wave through LDS (E % 8 == 0 and a 16-byte aligned w_gate): each k-step's 32 rows are loaded 16 bytes
+// a lane and written to the wave's stage in their own row-major layout, and the B fragments (8 consecutive h of
+// one expert) come out of ds_read_tr16_b64, which hands lane i of each 16-lane group element i % 4 of the
+// 4-element rows addressed by lanes 4 j + i / 4 (j < 4). Without LW every fragment is 8 strided 2-byte global
+// loads.
 template <int EB, int TB, bool LW>
 __global__ __launch_bounds__(waves_for(EB, TB) * kWave) void routing_topk_kernel(const uint16_t* __restrict__ x,
                                                                               const uint16_t* __restrict__ w_gate,
@@ -215,7 +219,7 @@ __global__ __launch_bounds__(waves_for(EB, TB) * kWave) void routing_topk_kernel
     constexpr int U = unroll_for(EB, TB);
     constexpr int Epad = EB * 16;
     constexpr int NT = 16 * TB;  // tokens per workgroup
-    // [W][NT tokens][Epad] fp32 partial logits (row (0, t) receives the fold); with LW then [W][U][32][Epad] fp16
+    // [W][NT tokens][Epad] fp32 partial logits (row (0, t) receives the fold); with LW then [W][32][Epad] fp16
     extern __shared__ float part[];
     const int lane = lane_id();
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);  // uniform: scalar loops
@@ -237,10 +241,8 @@ __global__ __launch_bounds__(waves_for(EB, TB) * kWave) void routing_topk_kernel
         for (int b = 0; b < EB; ++b) acc[tb][b] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     const int nsteps = H / 32;
-    // LW: this wave's U stages, the buffer resource over w_gate, and each lane's copy and fragment offsets
-    uint8_t* wst = reinterpret_cast<uint8_t*>(part + W * NT * Epad) + wave * (U * 32 * Epad * 2);
-    const __amdgpu_buffer_rsrc_t wrs =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(w_gate), 0, LW ? H * E * 2 : 0, 0x00020000);
+    // LW: this wave's stage, and each lane's chunk and fragment offsets
+    uint8_t* wst = reinterpret_cast<uint8_t*>(part + W * NT * Epad) + wave * (32 * Epad * 2);
     int cpy_off[EB];     // byte offset in w_gate (relative to the k-step's first row) of the chunk this lane copies
     int frag_off[2][EB]; // byte offset in a stage of the 8 bytes this lane addresses for half h of expert block b
     if constexpr (LW) {
@@ -261,31 +263,64 @@ __global__ __launch_bounds__(waves_for(EB, TB) * kWave) void routing_topk_kernel
                 frag_off[h][b] = wstage_chunk<EB>(r, e / 8) + (e % 8) * 2;
             }
     }
-    for (int s0 = wave; s0 < nsteps; s0 += U * W) {
-        f16x8 a[U][TB];
-        f16x8 bv[U][EB];
+    if constexpr (LW) {
+        // UL k-steps per round trip: their x fragments and w_gate chunks are all loaded into registers first (16
+        // bytes a lane each), then k-step by k-step the chunks are written to the wave's LDS stage (row-major,
+        // XOR-swizzled 16-byte chunks), read back as B fragments by ds_read_tr16_b64 and multiplied. The k-steps
+        // are added in the order s0, s0 + W, ... (Direct-to-LDS copies of the chunks were used here before: the
+        // compiler waits for every copy in flight before any LDS read, which held a round trip to 2 k-steps.)
+        constexpr int UL = lw_unroll(EB, TB);
+        const uint8_t* wbytes = reinterpret_cast<const uint8_t*>(w_gate);
+        for (int s0 = wave; s0 < nsteps; s0 += UL * W) {
+            f16x8 a[UL][TB];
+            u32x4 wv[UL][EB];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int s = s0 + u * W;
-            const bool in = s < nsteps;
-            const int k0 = (in ? s : 0) * 32;
+            for (int u = 0; u < UL; ++u) {
+                const int s = s0 + u * W;
+                const int k0 = (s < nsteps ? s : 0) * 32;  // a k-step past H loads k-step 0 and multiplies zeros
 #pragma unroll
-            for (int tb = 0; tb < TB; ++tb) {
-                a[u][tb] = load_f16x8(xrow[tb] + k0);
-                if (!in) {  // a k-step past H contributes nothing, whatever x holds (0 * inf would be NaN)
+                for (int tb = 0; tb < TB; ++tb) a[u][tb] = load_f16x8(xrow[tb] + k0);
 #pragma unroll
-                    for (int q = 0; q < 8; ++q) a[u][tb][q] = static_cast<f16>(0.0f);
-                }
+                for (int i = 0; i < EB; ++i)
+                    wv[u][i] = *reinterpret_cast<const u32x4*>(wbytes + static_cast<size_t>(k0) * E * 2 + cpy_off[i]);
             }
-            if constexpr (LW) {
-                if (in) {
+            __builtin_amdgcn_sched_barrier(0);  // all UL k-steps' loads are issued before the first is waited for
 #pragma unroll
-                    for (int i = 0; i < EB; ++i)
-                        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                            wrs, (__attribute__((address_space(3))) void*)(wst + (u * 32 * Epad * 2) + i * 1024), 16,
-                            static_cast<int>(cpy_off[i]), k0 * E * 2, 0, 0);  // (the cast keeps the host pass's launch stub)
+            for (int u = 0; u < UL; ++u) {
+                const bool in = s0 + u * W < nsteps;  // every step runs, so no load is moved behind a branch
+#pragma unroll
+                for (int i = 0; i < EB; ++i) *reinterpret_cast<u32x4*>(wst + i * 1024 + lane * 16) = wv[u][i];
+                f16x8 bv[EB];
+#pragma unroll
+                for (int b = 0; b < EB; ++b) {
+                    const s16x4 lo = lds_read_tr16(wst + frag_off[0][b]);
+                    const s16x4 hi = lds_read_tr16(wst + frag_off[1][b]);
+                    bv[b] = in ? __builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7))
+                               : f16x8{};
                 }
-            } else {
+#pragma unroll
+                for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+                    for (int b = 0; b < EB; ++b) acc[tb][b] = mfma16x16x32(a[u][tb], bv[b], acc[tb][b]);
+            }
+        }
+    } else {  // w_gate B fragments as 8 strided 2-byte loads each, U k-steps per round trip
+        for (int s0 = wave; s0 < nsteps; s0 += U * W) {
+            f16x8 a[U][TB];
+            f16x8 bv[U][EB];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int s = s0 + u * W;
+                const bool in = s < nsteps;
+                const int k0 = (in ? s : 0) * 32;
+#pragma unroll
+                for (int tb = 0; tb < TB; ++tb) {
+                    a[u][tb] = load_f16x8(xrow[tb] + k0);
+                    if (!in) {  // a k-step past H contributes nothing, whatever x holds (0 * inf would be NaN)
+#pragma unroll
+                        for (int q = 0; q < 8; ++q) a[u][tb][q] = static_cast<f16>(0.0f);
+                    }
+                }
                 const uint16_t* wrow = w_gate + static_cast<size_t>(k0 + kg * 8) * E;
 #pragma unroll
                 for (int b = 0; b < EB; ++b) {
@@ -296,31 +331,13 @@ __global__ __launch_bounds__(waves_for(EB, TB) * kWave) void routing_topk_kernel
                                                     : static_cast<f16>(0.0f);
                 }
             }
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+                    for (int b = 0; b < EB; ++b) acc[tb][b] = mfma16x16x32(a[u][tb], bv[u][b], acc[tb][b]);
         }
-        if constexpr (LW) {
-            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // this wave's stage copies have landed in LDS
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const bool in = s0 + u * W < nsteps;
-#pragma unroll
-                for (int b = 0; b < EB; ++b) {
-                    if (in) {
-                        const uint8_t* st = wst + u * 32 * Epad * 2;
-                        const s16x4 lo = lds_read_tr16(st + frag_off[0][b]);
-                        const s16x4 hi = lds_read_tr16(st + frag_off[1][b]);
-                        bv[u][b] = __builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-                    } else {
-                        bv[u][b] = f16x8{};
-                    }
-                }
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-#pragma unroll
-            for (int tb = 0; tb < TB; ++tb)
-#pragma unroll
-                for (int b = 0; b < EB; ++b) acc[tb][b] = mfma16x16x32(a[u][tb], bv[u][b], acc[tb][b]);
     }
     // D[token tb*16 + 4*kg + r][expert b*16 + row]
 #pragma unroll

@@ -96,17 +96,17 @@ def test_plans(lib):
     rp = lib_mod.RoutingPlan()
     assert lib.moe_routing_topk_plan(128, 2048, 16, 2, C.byref(rp)) == MOE_OK
     assert (rp.grid, rp.block, rp.tokens_per_block, rp.workspace_bytes) == (8, 1024, 16, 0)
-    # 16 waves x (16 tokens x 16 experts of fp32 partials + 4 w_gate stages of 32 rows x 16 fp16 experts)
-    assert rp.lds_bytes == 16 * (16 * 16 * 4 + 4 * 32 * 16 * 2)
+    # 16 waves x (16 tokens x 16 experts of fp32 partials + a w_gate stage of 32 rows x 16 fp16 experts)
+    assert rp.lds_bytes == 16 * (16 * 16 * 4 + 32 * 16 * 2)
     # 32 < E <= 64: 4 waves per 16 tokens, or per 2 blocks of 16 when T keeps 256 workgroups busy
     assert lib.moe_routing_topk_plan(2048, 2048, 64, 6, C.byref(rp)) == MOE_OK
-    # 4 waves x (16 tokens x 64 experts of fp32 partials + 4 w_gate stages of 32 rows x 64 fp16 experts)
-    assert (rp.grid, rp.block, rp.tokens_per_block, rp.lds_bytes) == (128, 256, 16, 4 * (16 * 64 * 4 + 4 * 32 * 64 * 2))
+    # 4 waves x (16 tokens x 64 experts of fp32 partials + a w_gate stage of 32 rows x 64 fp16 experts)
+    assert (rp.grid, rp.block, rp.tokens_per_block, rp.lds_bytes) == (128, 256, 16, 4 * (16 * 64 * 4 + 32 * 64 * 2))
     assert lib.moe_routing_topk_plan(16384, 2048, 64, 6, C.byref(rp)) == MOE_OK
-    # at most 2 token blocks for 32 < E <= 64, so two 64 KB workgroups share a CU
-    assert (rp.grid, rp.block, rp.tokens_per_block, rp.lds_bytes) == (512, 256, 32, 4 * (32 * 64 * 4 + 2 * 32 * 64 * 2))
+    # at most 2 token blocks for 32 < E <= 64, so two 48 KB workgroups share a CU
+    assert (rp.grid, rp.block, rp.tokens_per_block, rp.lds_bytes) == (512, 256, 32, 4 * (32 * 64 * 4 + 32 * 64 * 2))
     assert lib.moe_routing_topk_plan(8192, 2048, 16, 2, C.byref(rp)) == MOE_OK
-    assert (rp.grid, rp.block, rp.tokens_per_block, rp.lds_bytes) == (256, 1024, 32, 16 * (32 * 16 * 4 + 4 * 32 * 16 * 2))
+    assert (rp.grid, rp.block, rp.tokens_per_block, rp.lds_bytes) == (256, 1024, 32, 16 * (32 * 16 * 4 + 32 * 16 * 2))
     # E > 64: 64 tokens per workgroup; the rows kernel (4 waves of 16 tokens over all of H, four 16 KB w_gate
     # stages, each wave's x ring of 16 + 1 k-steps of 1 KB)
     assert lib.moe_routing_topk_plan(16384, 2048, 256, 8, C.byref(rp)) == MOE_OK

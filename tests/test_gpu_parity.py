@@ -855,6 +855,52 @@ def test_layer_on_a_side_stream(ops):
         assert torch.equal(eo_f, eo_s) and torch.equal(y_f, y_s)
 
 
+def test_concurrent_threads_and_streams(ops):
+    """Two host threads, each queueing three layers on its own stream with no synchronisation in between, one on
+    each FFN schedule, both through the three operators and through moe_layer. The calls are re-entrant: the
+    kernel-attribute and occupancy caches are mutex-guarded, the last error is per thread and every buffer is the
+    caller's. Every output equals a sequential run bit for bit."""
+    import threading
+    cases = ((64, 256, 8, 2, 512), (600, 128, 8, 3, 128))
+    data, refs = [], []
+    for T, H, E, K, I in cases:
+        gen = torch.Generator(device="cpu").manual_seed(T + 7)
+        x = torch.randn(T, H, generator=gen).half().cuda()
+        wg = (torch.randn(H, E, generator=gen) / math.sqrt(H)).half().cuda()
+        ew = (torch.randn(E, 3 * I, H, generator=gen) / math.sqrt(H)).half().cuda()
+        data.append((x, wg, ew, K))
+        refs.append((ops.moe_layer(x, wg, ew, K), ops.moe_layer_fused(x, wg, ew, K)))
+    torch.cuda.synchronize()
+    results, errors = [None] * len(cases), []
+
+    def worker(c):
+        try:
+            x, wg, ew, K = data[c]
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.default_stream())
+            with torch.cuda.stream(s):  # this thread's allocations belong to its stream
+                outs = [(ops.moe_layer(x, wg, ew, K, stream=s), ops.moe_layer_fused(x, wg, ew, K, stream=s))
+                        for _ in range(3)]
+            s.synchronize()
+            results[c] = outs
+        except Exception as exc:  # re-raised in the main thread
+            errors.append(exc)
+
+    threads = [threading.Thread(target=worker, args=(c,)) for c in range(len(cases))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    if errors:
+        raise errors[0]
+    for c, (T, H, E, K, I) in enumerate(cases):
+        log(f"[threads] T={T} H={H} E={E} K={K} I={I} schedule={ffn_schedule(T, H, E, K, I)}")
+        for three_op, fused in results[c]:
+            for got, ref in ((three_op, refs[c][0]), (fused, refs[c][1])):
+                for a, b in zip(got, ref):
+                    assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize("T,H,E,K,I,schedule", [
     (64, 256, 8, 2, 512, 0),       # weight streaming: routing, then the FFN with the combine in its reduce
     (1000, 128, 8, 2, 128, 1),     # tiled; routing 16-token blocks of 16 waves, w_gate through LDS
