@@ -37,8 +37,8 @@ int ffn_schedule(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
 // Layout (each region 256-byte aligned): offsets [E+1] i32 | sorted_slot [T*K] i32 | hidden [T*K, I] fp16, then
 // for the weight-streaming schedule: partial [nsplit, T*K, H] fp32 (when the down projection is split over K) |
 // slot_row [T*K] i32; for the tiled schedule: the permute's scratch (rank [T*K] i32, counts [chunks, E] i32),
-// then with tiled_split up to 256 fp32 partial tiles of 256 x 256 (64 MiB; one per workgroup of the down launch,
-// none when I < 256) for the leftover round it splits over k.
+// then with tiled_split up to 256 fp32 partial tiles of 256 x 256 (64 MiB; one per workgroup of the down launch)
+// for the leftover round it splits over k (none when I < 256 or when the down tiles fill more than 4 rounds).
 size_t ffn_workspace_bytes(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I, bool tiled_split) {
     const size_t S = static_cast<size_t>(T) * static_cast<size_t>(K);
     size_t bytes = align_up(sizeof(int32_t) * static_cast<size_t>(E + 1), 256);

@@ -4,7 +4,7 @@
  * Drop-in for the three CANN operators of Lu-Yu-Zhen/Implementing-MoE-Architecture-Operators-on-CANN-Platform:
  *   MoeRoutingTopK -> MoeExpertFFN -> MoeCombine
  * Each CANN operator is one OpDef (prototype) + InferShape + InferDataType + TilingFunc in
- * op_host/moe_ops.cpp, and one kernel entry point in op_kernel/*.cpp. Here each becomes a set of plain C
+ * op_host/moe_ops.cpp, and one kernel entry point in the op_kernel/ sources. Here each becomes a set of plain C
  * functions: *_infer_shape / *_infer_dtype (graph-time), *_plan (launch planning) and the launch itself.
  *
  * Conventions (kept from the reference, op_host/moe_ops.cpp and tests/test_moe.cpp:415-463):
@@ -119,7 +119,8 @@ moe_status moe_expert_ffn_infer_dtype(moe_dtype* expert_out_dtype);
 /* Workspace bytes for one call (TilingFunc workspace, op_host/moe_ops.cpp:340-349). Holds the expert-sorted
  * slot order, per-expert offsets and the fp16 SwiGLU intermediate [T*K, I]; on the weight-streaming schedule
  * also the split-K partial sums and the slot -> sorted-row map; on the LDS-tiled schedule also up to 64 MiB of
- * fp32 partial tiles for the tiles it splits over k. 0 for invalid sizes. */
+ * fp32 partial tiles for the tiles it splits over k (only when its down tiles fill at most 4 rounds of the
+ * GPU). 0 for invalid sizes. */
 size_t moe_expert_ffn_workspace_bytes(int64_t num_tokens, int64_t hidden_size, int64_t num_experts,
                                       int64_t top_k, int64_t intermediate_size);
 
