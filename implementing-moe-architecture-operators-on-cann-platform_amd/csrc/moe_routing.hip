@@ -28,6 +28,8 @@
 // multiplied, two LDS buffers, one barrier per stage.
 // HBM traffic per launch: T*H*2 (x) + H*E*2 (w_gate, L2-resident after the first workgroups) + T*K*6 bytes.
 
+#include <type_traits>
+
 #include "moe_device.h"
 #include "moe_launch.h"
 #include "moe_slot_rank.h"
@@ -271,13 +273,16 @@ __global__ __launch_bounds__(waves_for(EB, TB) * kWave) void routing_topk_kernel
         // compiler waits for every copy in flight before any LDS read, which held a round trip to 2 k-steps.)
         constexpr int UL = lw_unroll(EB, TB);
         const uint8_t* wbytes = reinterpret_cast<const uint8_t*>(w_gate);
-        for (int s0 = wave; s0 < nsteps; s0 += UL * W) {
+        // FULL: all UL k-steps of the round exist; the last round of a wave may run past H, and its extra k-steps
+        // load k-step 0 and multiply zeros (every step runs, so no load is moved behind a branch)
+        auto round = [&](int s0, auto full) __attribute__((always_inline)) {
+            constexpr bool FULL = decltype(full)::value;
             f16x8 a[UL][TB];
             u32x4 wv[UL][EB];
 #pragma unroll
             for (int u = 0; u < UL; ++u) {
                 const int s = s0 + u * W;
-                const int k0 = (s < nsteps ? s : 0) * 32;  // a k-step past H loads k-step 0 and multiplies zeros
+                const int k0 = (FULL || s < nsteps ? s : 0) * 32;
 #pragma unroll
                 for (int tb = 0; tb < TB; ++tb) a[u][tb] = load_f16x8(xrow[tb] + k0);
 #pragma unroll
@@ -287,7 +292,7 @@ __global__ __launch_bounds__(waves_for(EB, TB) * kWave) void routing_topk_kernel
             __builtin_amdgcn_sched_barrier(0);  // all UL k-steps' loads are issued before the first is waited for
 #pragma unroll
             for (int u = 0; u < UL; ++u) {
-                const bool in = s0 + u * W < nsteps;  // every step runs, so no load is moved behind a branch
+                const bool in = FULL || s0 + u * W < nsteps;
 #pragma unroll
                 for (int i = 0; i < EB; ++i) *reinterpret_cast<u32x4*>(wst + i * 1024 + lane * 16) = wv[u][i];
                 f16x8 bv[EB];
@@ -303,7 +308,10 @@ __global__ __launch_bounds__(waves_for(EB, TB) * kWave) void routing_topk_kernel
 #pragma unroll
                     for (int b = 0; b < EB; ++b) acc[tb][b] = mfma16x16x32(a[u][tb], bv[b], acc[tb][b]);
             }
-        }
+        };
+        int s0 = wave;
+        for (; s0 + (UL - 1) * W < nsteps; s0 += UL * W) round(s0, std::true_type{});
+        if (s0 < nsteps) round(s0, std::false_type{});
     } else {  // w_gate B fragments as 8 strided 2-byte loads each, U k-steps per round trip
         for (int s0 = wave; s0 < nsteps; s0 += U * W) {
             f16x8 a[U][TB];
