@@ -14,8 +14,9 @@
 //            decode, H = 2048 and W = 16: 4 k-steps a wave), else it issues the loads of U k-steps per round trip;
 //            it keeps partial logits of every expert block in registers and parks them in LDS.
 //   Fold:    one thread per (token, expert) adds the W partials in wave order.
-//   Phase 2: one 16-lane DPP row per token (each lane holding Epad / 16 experts; four tokens per wave at a time)
-//            runs the softmax, top-K and renormalisation with all-reduces over the row (select_row): max,
+//   Phase 2: one 16-lane DPP row per token for E <= 16, half a row (8 lanes) for larger E (each lane holding
+//            Epad / 16 or Epad / 8 experts; 4 or 8 tokens per wave at a time) runs the softmax, top-K and
+//            renormalisation with all-reduces over the token's lanes (select_row): max,
 //            expf(l - max), sum, division by the sum; K rounds of an arg-max (lowest index wins an exact tie); the
 //            renormalising sum over the K picks in rank order; fp16 round-to-nearest-even.
 // For E > 64 the rows kernel runs: a workgroup owns 64 tokens and each of its 4 waves 16 of them over all of H,
@@ -40,6 +41,10 @@ namespace {
 
 constexpr int kTokensPerBlock = 16;
 constexpr int kSelLanes = 16;  // lanes that select one token's experts (phase 2): one DPP row
+// The narrow kernel's lanes per token: half a DPP row for E > 16. Fewer lanes per token each hold more experts,
+// so the 64-bit arg-max steps cover twice the tokens per wave. DeepSeek shape (E = 64, K = 6): 20.7 against 21.6 us;
+// at E = 16 (one expert per lane) 8 lanes were slower (decode 5.44 against 5.28 us); 4 lanes at E = 64 took 22.8 us.
+constexpr int narrow_sel_lanes(int eb) { return eb == 1 ? 16 : 8; }
 
 // The narrow kernel runs E <= 64. The wave count fixes each token's summation order (wave w adds the k-steps
 // w, w + W, ... and the partials are folded in wave order), so it does not depend on the token blocks: a token's
@@ -76,7 +81,8 @@ bool narrow_lds_weights(const void* w_gate, int H, int E) {
 // The 16-lane all-reduce runs on DPP row operations (a VALU operand modifier, no LDS round trip). Step 0 pairs
 // lane i with i ^ 1 and step 1 with i ^ 2 (quad permutes); step 2 mirrors each half row (i <-> 7 - i, which
 // pairs the two quads of the half, each already uniform) and step 3 the row (i <-> 15 - i, pairing the halves).
-// Every lane ends with the row's result and the association is the same as a xor-1/2/4/8 butterfly's.
+// Every lane ends with the row's result and the association is the same as a xor-1/2/4/8 butterfly's. Steps 0-2
+// alone all-reduce each half row (8 lanes), like a xor-1/2/4 butterfly.
 template <int STEP>
 __device__ __forceinline__ int row_partner(int v) {
     constexpr int ctrl = STEP == 0 ? 0xB1 : STEP == 1 ? 0x4E : STEP == 2 ? 0x141 : 0x140;
@@ -87,55 +93,23 @@ __device__ __forceinline__ float row_partner(float v) {
     return __builtin_bit_cast(float, row_partner<STEP>(__builtin_bit_cast(int, v)));
 }
 
-// Softmax, top-K and renormalisation of one token per 16-lane DPP row (four tokens per wave); row lane gl holds
-// experts gl + 16 q, q < EPL, of the token's logits row (fp32, in LDS). The max and the arg-max (lowest index
-// wins an exact tie, as the reference's strict '>' scans) are exact in any order; the softmax sum adds in one
-// fixed association, identical in every lane of the row, so a token's result does not depend on its batch.
-// Probabilities are exp(l - max) / sum, the K picks come in descending order, and their renormalisation sums
-// them in rank order (the oracle's order, tests/moe_cpu_sim.cpp:224-243); lane gl writes picks gl, gl + 16, ...
-// below K. All 64 lanes of the wave must call this (DPP reads the neighbours' registers); only rows with
-// `active` set write.
-// select_vals takes the lane's logits v[q] (expert gl + 16 q) from registers; select_row reads them from an LDS
+// Softmax, top-K and renormalisation of one token per group of G lanes (a DPP row, G = 16, or half of one, G = 8;
+// 64 / G tokens per wave); group lane gl holds experts gl + G q, q < EPL, of the token's logits row. The max and
+// the arg-max (lowest index wins an exact tie, as the reference's strict '>' scans) are exact in any order; the
+// softmax sum adds in one fixed association for a given G, identical in every lane of the group, so a token's
+// result does not depend on its batch. Probabilities are exp(l - max) / sum, the K picks come in descending
+// order, and their renormalisation sums them in rank order (the oracle's order, tests/moe_cpu_sim.cpp:224-243);
+// lane gl writes picks gl, gl + G, ... below K. All 64 lanes of the wave must call this (DPP reads the
+// neighbours' registers); only groups with `active` set write.
+// select_vals takes the lane's logits v[q] (expert gl + G q) from registers; select_row reads them from an LDS
 // row of the token's logits.
-template <int EPL>
-__device__ __forceinline__ void select_vals(float (&v)[EPL], int E, int K, bool active, int32_t* ids_out,
-                                            uint16_t* w_out) {
-    constexpr int G = kSelLanes;
+//
+// The K rounds of arg-max over the 64-bit keys. Pick k sits in lane k % G, slot k / G of my_key; NP = 1 when
+// K <= G (every lane holds at most one pick), else EPL (K <= E <= G EPL).
+template <int EPL, int G, int NP>
+__device__ __forceinline__ void pick_topk(uint64_t (&key)[EPL], int K, bool active, int32_t* ids_out,
+                                          uint16_t* w_out) {
     const int gl = lane_id() & (G - 1);
-    float mx = -1e30f;  // the oracle's starting maximum
-#pragma unroll
-    for (int q = 0; q < EPL; ++q) {
-        const int e = gl + G * q;
-        v[q] = e < E ? v[q] : -1e30f;
-        mx = fmaxf(mx, v[q]);
-    }
-    mx = fmaxf(mx, row_partner<0>(mx));
-    mx = fmaxf(mx, row_partner<1>(mx));
-    mx = fmaxf(mx, row_partner<2>(mx));
-    mx = fmaxf(mx, row_partner<3>(mx));
-    float total = 0.0f;
-#pragma unroll
-    for (int q = 0; q < EPL; ++q) {
-        v[q] = gl + G * q < E ? expf(v[q] - mx) : 0.0f;
-        total += v[q];
-    }
-    total += row_partner<0>(total);
-    total += row_partner<1>(total);
-    total += row_partner<2>(total);
-    total += row_partner<3>(total);
-    // One 64-bit key per candidate: the probability's bits + 1 above, the complemented expert index below. For
-    // p >= 0 the bits order like the values, so the largest key is the largest probability and, among exact
-    // ties, the lowest index (the reference's strict '>' scan in index order). Padding experts, NaN and picked
-    // experts hold a zero upper word, below every candidate.
-    uint64_t key[EPL];
-#pragma unroll
-    for (int q = 0; q < EPL; ++q) {
-        const int e = gl + G * q;
-        const float pq = v[q] / total;
-        const uint32_t hi = e < E && pq == pq ? __builtin_bit_cast(uint32_t, pq) + 1u : 0u;  // NaN never wins
-        key[q] = (static_cast<uint64_t>(hi) << 32) | static_cast<uint32_t>(~e);
-    }
-    constexpr int NP = EPL;  // K <= E <= 16 EPL picks; pick k sits in lane k % 16, slot k / 16
     float sel = 0.0f;
     uint64_t my_key[NP];
 #pragma unroll
@@ -145,7 +119,7 @@ __device__ __forceinline__ void select_vals(float (&v)[EPL], int E, int K, bool 
 #pragma unroll
         for (int q = 1; q < EPL; ++q) best = key[q] > best ? key[q] : best;
 #pragma unroll
-        for (int st = 0; st < 4; ++st) {
+        for (int st = 0; st < (G == 16 ? 4 : 3); ++st) {
             const uint32_t lo = static_cast<uint32_t>(best), hi = static_cast<uint32_t>(best >> 32);
             const uint32_t olo = static_cast<uint32_t>(st == 0   ? row_partner<0>(static_cast<int>(lo))
                                                        : st == 1 ? row_partner<1>(static_cast<int>(lo))
@@ -161,9 +135,13 @@ __device__ __forceinline__ void select_vals(float (&v)[EPL], int E, int K, bool 
 #pragma unroll
         for (int q = 0; q < EPL; ++q)  // keys are unique (the index part): exactly one lane owns the pick
             key[q] = key[q] == best ? static_cast<uint64_t>(static_cast<uint32_t>(key[q])) : key[q];
+        if constexpr (NP == 1) {
+            if ((k & (G - 1)) == gl) my_key[0] = best;
+        } else {
 #pragma unroll
-        for (int j = 0; j < NP; ++j)
-            if ((k >> 4) == j && (k & (G - 1)) == gl) my_key[j] = best;  // the first test is uniform
+            for (int j = 0; j < NP; ++j)
+                if (k / G == j && (k & (G - 1)) == gl) my_key[j] = best;  // the first test is uniform
+        }
         sel += __builtin_bit_cast(float, static_cast<uint32_t>(best >> 32) - 1u);
     }
     if (active) {
@@ -178,14 +156,58 @@ __device__ __forceinline__ void select_vals(float (&v)[EPL], int E, int K, bool 
     }
 }
 
-template <int EPL>
+template <int EPL, int G = kSelLanes>
+__device__ __forceinline__ void select_vals(float (&v)[EPL], int E, int K, bool active, int32_t* ids_out,
+                                            uint16_t* w_out) {
+    static_assert(G == 8 || G == 16, "a token's lanes: half a DPP row or a whole one");
+    const int gl = lane_id() & (G - 1);
+    float mx = -1e30f;  // the oracle's starting maximum
+#pragma unroll
+    for (int q = 0; q < EPL; ++q) {
+        const int e = gl + G * q;
+        v[q] = e < E ? v[q] : -1e30f;
+        mx = fmaxf(mx, v[q]);
+    }
+    mx = fmaxf(mx, row_partner<0>(mx));
+    mx = fmaxf(mx, row_partner<1>(mx));
+    mx = fmaxf(mx, row_partner<2>(mx));
+    if constexpr (G == 16) mx = fmaxf(mx, row_partner<3>(mx));
+    float total = 0.0f;
+#pragma unroll
+    for (int q = 0; q < EPL; ++q) {
+        v[q] = gl + G * q < E ? expf(v[q] - mx) : 0.0f;
+        total += v[q];
+    }
+    total += row_partner<0>(total);
+    total += row_partner<1>(total);
+    total += row_partner<2>(total);
+    if constexpr (G == 16) total += row_partner<3>(total);
+    // One 64-bit key per candidate: the probability's bits + 1 above, the complemented expert index below. For
+    // p >= 0 the bits order like the values, so the largest key is the largest probability and, among exact
+    // ties, the lowest index (the reference's strict '>' scan in index order). Padding experts, NaN and picked
+    // experts hold a zero upper word, below every candidate.
+    uint64_t key[EPL];
+#pragma unroll
+    for (int q = 0; q < EPL; ++q) {
+        const int e = gl + G * q;
+        const float pq = v[q] / total;
+        const uint32_t hi = e < E && pq == pq ? __builtin_bit_cast(uint32_t, pq) + 1u : 0u;  // NaN never wins
+        key[q] = (static_cast<uint64_t>(hi) << 32) | static_cast<uint32_t>(~e);
+    }
+    if (K <= G)
+        pick_topk<EPL, G, 1>(key, K, active, ids_out, w_out);
+    else
+        pick_topk<EPL, G, EPL>(key, K, active, ids_out, w_out);
+}
+
+template <int EPL, int G = kSelLanes>
 __device__ __forceinline__ void select_row(const float* row, int E, int K, bool active, int32_t* ids_out,
                                            uint16_t* w_out) {
-    const int gl = lane_id() & (kSelLanes - 1);
+    const int gl = lane_id() & (G - 1);
     float v[EPL];
 #pragma unroll
-    for (int q = 0; q < EPL; ++q) v[q] = gl + kSelLanes * q < E ? row[gl + kSelLanes * q] : 0.0f;
-    select_vals<EPL>(v, E, K, active, ids_out, w_out);
+    for (int q = 0; q < EPL; ++q) v[q] = gl + G * q < E ? row[gl + G * q] : 0.0f;
+    select_vals<EPL, G>(v, E, K, active, ids_out, w_out);
 }
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -366,13 +388,14 @@ __global__ __launch_bounds__(waves_for(EB, TB) * kWave) void routing_topk_kernel
     }
     __syncthreads();
 
-    // ---- phase 2: 16 lanes per token (EB experts a lane), 4 tokens per wave at a time ----
-    constexpr int TPW = kWave / kSelLanes;  // tokens per wave and round
+    // ---- phase 2: G lanes per token (Epad / G experts a lane), 64 / G tokens per wave at a time ----
+    constexpr int G = narrow_sel_lanes(EB);
+    constexpr int TPW = kWave / G;  // tokens per wave and round
     for (int tb = wave * TPW; tb < NT; tb += W * TPW) {
-        const int t = tb + lane / kSelLanes;
+        const int t = tb + lane / G;
         const bool active = t < NT && t0 + t < T;
         const int tr = min(t, NT - 1);  // inactive groups read a valid row and write nothing
-        select_row<EB>(part + tr * Epad, E, K, active, expert_ids + static_cast<size_t>(t0 + tr) * K,
+        select_row<Epad / G, G>(part + tr * Epad, E, K, active, expert_ids + static_cast<size_t>(t0 + tr) * K,
                        weights + static_cast<size_t>(t0 + tr) * K);
     }
     // ---- optional tail: the block's slots ranked by expert, for the permute's scatter ----
