@@ -115,9 +115,15 @@ __device__ __forceinline__ void pick_topk(uint64_t (&key)[EPL], int K, bool acti
 #pragma unroll
     for (int j = 0; j < NP; ++j) my_key[j] = 0;
     for (int k = 0; k < K; ++k) {
-        uint64_t best = key[0];
+        // the lane's own maximum as a pairwise tree (independent compares issue back to back)
+        uint64_t tr[EPL];
 #pragma unroll
-        for (int q = 1; q < EPL; ++q) best = key[q] > best ? key[q] : best;
+        for (int q = 0; q < EPL; ++q) tr[q] = key[q];
+#pragma unroll
+        for (int w = 1; w < EPL; w *= 2)
+#pragma unroll
+            for (int q = 0; q + w < EPL; q += 2 * w) tr[q] = tr[q + w] > tr[q] ? tr[q + w] : tr[q];
+        uint64_t best = tr[0];
 #pragma unroll
         for (int st = 0; st < (G == 16 ? 4 : 3); ++st) {
             const uint32_t lo = static_cast<uint32_t>(best), hi = static_cast<uint32_t>(best >> 32);
@@ -133,8 +139,10 @@ __device__ __forceinline__ void pick_topk(uint64_t (&key)[EPL], int K, bool acti
             best = other > best ? other : best;
         }
 #pragma unroll
-        for (int q = 0; q < EPL; ++q)  // keys are unique (the index part): exactly one lane owns the pick
-            key[q] = key[q] == best ? static_cast<uint64_t>(static_cast<uint32_t>(key[q])) : key[q];
+        for (int q = 0; q < EPL; ++q)  // the index part alone is unique: exactly one lane owns the pick
+            key[q] = static_cast<uint32_t>(key[q]) == static_cast<uint32_t>(best)
+                         ? static_cast<uint64_t>(static_cast<uint32_t>(key[q]))
+                         : key[q];
         if constexpr (NP == 1) {
             if ((k & (G - 1)) == gl) my_key[0] = best;
         } else {
