@@ -457,7 +457,35 @@ __global__ __launch_bounds__(kThreads) void ffn_stream_kernel(StreamArgs p, int 
     }
 }
 
+// The split reduce's loads: the 8 columns c.. of row `row` in splits s0 .. s0 + kSplitBatch - 1, issued together
+// (split indices past the last read the last split again, always in bounds), then added into acc in split order:
+// acc = ((p0 + p1) + p2) + ... whatever the batching. The adds are selects, not branches, so the compiler cannot
+// move a split's loads behind its own test and wait for each split in turn.
+constexpr int kSplitBatch = 4;
+__device__ __forceinline__ void add_split_batch(const float* __restrict__ partial, size_t split_stride, size_t row_off,
+                                                int s0, int nsplit, float (&acc)[8]) {
+    f32x4 v[kSplitBatch][2];
+#pragma unroll
+    for (int u = 0; u < kSplitBatch; ++u) {
+        const f32x4* src = reinterpret_cast<const f32x4*>(partial + static_cast<size_t>(min(s0 + u, nsplit - 1)) *
+                                                                        split_stride + row_off);
+        v[u][0] = src[0];
+        v[u][1] = src[1];
+    }
+#pragma unroll
+    for (int u = 0; u < kSplitBatch; ++u) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float x = v[u][j / 4][j % 4];
+            const float sum = s0 + u == 0 ? x : acc[j] + x;
+            acc[j] = s0 + u < nsplit ? sum : acc[j];
+        }
+    }
+}
+
 // expert_out[sorted_slot[r], h] = fp16(((partial[0][r][h] + partial[1][r][h]) + ...)), 8 columns per thread.
+// Every row r < total_rows lies inside the partial buffer and sorted_slot, so the loads go out before the
+// valid-row bound is known; rows past it (ids outside [0, E)) are dropped afterwards.
 __global__ __launch_bounds__(256) void down_reduce_kernel(const float* __restrict__ partial,
                                                           const int32_t* __restrict__ sorted_slot,
                                                           const int32_t* __restrict__ offsets, int E, int total_rows,
@@ -467,20 +495,18 @@ __global__ __launch_bounds__(256) void down_reduce_kernel(const float* __restric
     if (idx >= static_cast<int64_t>(total_rows) * vec) return;
     const int r = static_cast<int>(idx / vec);
     const int c = static_cast<int>(idx % vec) * 8;
-    if (r >= offsets[E]) return;  // rows past the valid ones (ids outside [0, E)) belong to no expert
+    const int slot = sorted_slot[r];
+    const int valid_rows = offsets[E];
     float acc[8];
-    const float* src = partial + static_cast<size_t>(r) * H + c;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[j] = src[j];
-    for (int s = 1; s < nsplit; ++s) {
-        const float* ps = src + static_cast<size_t>(s) * total_rows * H;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[j] += ps[j];
-    }
+    for (int s0 = 0; s0 < nsplit; s0 += kSplitBatch)
+        add_split_batch(partial, static_cast<size_t>(total_rows) * H, static_cast<size_t>(r) * H + c, s0, nsplit, acc);
     f16x8 o;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) o[j] = static_cast<f16>(acc[j]);
-    *reinterpret_cast<f16x8*>(expert_out + static_cast<size_t>(sorted_slot[r]) * H + c) = o;
+    for (int j = 0; j < 8; ++j) {
+        o[j] = static_cast<f16>(acc[j]);
+        asm volatile("" ::"v"(o[j]));  // computed here, not behind the row test below
+    }
+    if (r < valid_rows) *reinterpret_cast<f16x8*>(expert_out + static_cast<size_t>(slot) * H + c) = o;
 }
 
 // The split reduce fused with MoeCombine, one thread per (token, 8 columns): for k ascending, expert_out row
@@ -488,6 +514,9 @@ __global__ __launch_bounds__(256) void down_reduce_kernel(const float* __restric
 // y[t] = sum_k weights[t, k] * expert_out[t, k] with the combine kernel's fp32 arithmetic (accumulator from 0,
 // k ascending, no contraction), so y is bit-identical to MoeCombine on that expert_out. Rows of ids outside
 // [0, E) are the zero rows the gate/up kernel wrote, and enter the sum as zeros, as they do in MoeCombine.
+// The slots are taken kKBatch at a time: their ids, sorted rows and weights are loaded together, then all
+// their partials (slot_row holds a row only for valid ids; the others read row 0, in bounds, and are dropped).
+constexpr int kKBatch = 2;
 __global__ __launch_bounds__(256) void reduce_combine_kernel(const float* __restrict__ partial,
                                                              const int32_t* __restrict__ slot_row,
                                                              const int32_t* __restrict__ ids,
@@ -504,30 +533,42 @@ __global__ __launch_bounds__(256) void reduce_combine_kernel(const float* __rest
     float yacc[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) yacc[j] = 0.0f;
-    for (int k = 0; k < K; ++k) {
-        const int sl = t * K + k;
-        const int id = ids[sl];
-        f16x8 o;
-        if (id >= 0 && id < E) {
-            const float* src = partial + static_cast<size_t>(slot_row[sl]) * H + c;
-            float acc[8];
+    for (int k0 = 0; k0 < K; k0 += kKBatch) {
+        bool valid[kKBatch];
+        int id[kKBatch], srow[kKBatch], row[kKBatch];
+        float w[kKBatch];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) acc[j] = src[j];
-            for (int s = 1; s < nsplit; ++s) {
-                const float* ps = src + static_cast<size_t>(s) * total_rows * H;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) acc[j] += ps[j];
-            }
-#pragma unroll
-            for (int j = 0; j < 8; ++j) o[j] = static_cast<f16>(acc[j]);
-            *reinterpret_cast<f16x8*>(expert_out + static_cast<size_t>(sl) * H + c) = o;
-        } else {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) o[j] = static_cast<f16>(0.0f);
+        for (int u = 0; u < kKBatch; ++u) {
+            const int sl = t * K + min(k0 + u, K - 1);
+            id[u] = ids[sl];
+            srow[u] = slot_row[sl];
+            w[u] = f16_bits_to_f32(weights[sl]);
         }
-        const float w = f16_bits_to_f32(weights[sl]);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) yacc[j] = yacc[j] + w * static_cast<float>(o[j]);
+        for (int u = 0; u < kKBatch; ++u) {
+            asm volatile("" ::"v"(srow[u]));  // loaded here with the ids, not behind a test of them
+            valid[u] = k0 + u < K && id[u] >= 0 && id[u] < E;
+            row[u] = valid[u] ? srow[u] : 0;
+        }
+        float acc[kKBatch][8];
+        for (int s0 = 0; s0 < nsplit; s0 += kSplitBatch) {
+#pragma unroll
+            for (int u = 0; u < kKBatch; ++u)
+                add_split_batch(partial, total_rows * H, static_cast<size_t>(row[u]) * H + c, s0, nsplit, acc[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < kKBatch; ++u) {
+            const bool in = k0 + u < K;  // uniform; selects rather than a branch (see add_split_batch)
+            f16x8 o;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o[j] = static_cast<f16>(valid[u] ? acc[u][j] : 0.0f);
+            if (valid[u]) *reinterpret_cast<f16x8*>(expert_out + (static_cast<size_t>(t) * K + k0 + u) * H + c) = o;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float sum = yacc[j] + w[u] * static_cast<float>(o[j]);
+                yacc[j] = in ? sum : yacc[j];
+            }
+        }
     }
     f16x8 out;
 #pragma unroll
