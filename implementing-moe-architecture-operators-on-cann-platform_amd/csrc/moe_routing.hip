@@ -586,10 +586,11 @@ __global__ __launch_bounds__(kRowWaves * kWave) void routing_rows_kernel(const u
 
     const __amdgpu_buffer_rsrc_t wrs =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(w_gate), 0, H * E * 2, 0x00020000);
-    const __amdgpu_buffer_rsrc_t xrs =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(x), 0, T * H * 2, 0x00020000);
+    // x rows of this workgroup's tokens only (at most kRowTokens rows: 32-bit offsets for any T)
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(x + static_cast<size_t>(t0) * H), 0, min(kRowTokens, T - t0) * H * 2, 0x00020000);
     // x copy: lane -> row lane / 4 (token t0 + 16 wave + row, clamped into the batch), 16-byte chunk lane % 4
-    const int xoff = (min(t0 + wave * 16 + lane / 4, T - 1) * H + (lane % 4) * 8) * 2;
+    const int xoff = (min(wave * 16 + lane / 4, T - 1 - t0) * H + (lane % 4) * 8) * 2;
     // w_gate copy: wave w fills 1 KB slabs w, w + 4, w + 8, w + 12 of a stage; lane -> 16-byte slot of the slab
     int woff[4];
 #pragma unroll
@@ -748,14 +749,14 @@ hipError_t launch_rows(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, 
 }
 
 // Which kernel routes: the narrow kernel for E <= 64; for E > 64 the rows kernel when its copies can run (lw:
-// w_gate rows can be copied 16 bytes at a time; x within 32-bit buffer offsets), else the wide kernel. The choice
-// does not depend on T.
+// w_gate rows can be copied 16 bytes at a time, and whole stages of k-steps), else the wide kernel. The choice
+// does not depend on T, so a token's ids and weights do not depend on the batch it is routed in.
 enum RoutingKernel { kNarrowKernel, kWideKernel, kRowsKernel };
 RoutingKernel routing_kernel(int T, int H, int E, bool lw) {
+    (void)T;
     const int eb = routing_expert_blocks(E);
     if (eb <= 4) return kNarrowKernel;
-    const bool rows_ok = lw && (H / 32) % row_stage_ksteps(eb) == 0 &&
-                         static_cast<int64_t>(T) * H * 2 < (int64_t{1} << 31);
+    const bool rows_ok = lw && (H / 32) % row_stage_ksteps(eb) == 0;
     return rows_ok ? kRowsKernel : kWideKernel;
 }
 

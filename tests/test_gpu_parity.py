@@ -319,6 +319,29 @@ def test_routing_is_batch_invariant(ops, E, K):
     assert np.array_equal(host(w_all)[:1000].view(np.uint16), host(w_few).view(np.uint16))
 
 
+def test_routing_rows_kernel_past_2gib_of_x(ops):
+    """E > 64 with x past 2 GiB (T = 2^19 + 80, H = 2048): the rows kernel addresses each workgroup's own x rows,
+    so it still runs and a token's ids and weights are the same bits as when its workgroup's tokens are routed
+    alone. The first and the last (partial) token blocks are also checked against the oracle."""
+    T, H, E, K = (1 << 19) + 80, 2048, 128, 8
+    assert T * H * 2 >= 1 << 31
+    log(f"[rows past 2 GiB] T={T} H={H} E={E} K={K}")
+    x = torch.empty((T, H), dtype=torch.float16, device="cuda")
+    ops.synth_normal_f16_(x, 17, synth.STREAM_X, 1.0)
+    rng = np.random.default_rng(17)
+    wg = (rng.standard_normal((H, E)) / math.sqrt(H)).astype(np.float16)
+    wg_d = dev(wg)
+    ids_all, w_all = ops.MoeRoutingTopK(x, wg_d, K)
+    ids_all, w_all = host(ids_all), host(w_all)
+    for lo, hi in ((0, 64), (T - 80, T)):
+        ids_few, w_few = ops.MoeRoutingTopK(x[lo:hi].contiguous(), wg_d, K)
+        assert np.array_equal(ids_all[lo:hi], host(ids_few))
+        assert np.array_equal(w_all[lo:hi].view(np.uint16), host(w_few).view(np.uint16))
+        check_routing(ids_all[lo:hi], w_all[lo:hi], host(x[lo:hi]), wg, K, f"rows past 2 GiB tokens {lo}-{hi}")
+    del x
+    torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("T,H,E,K", [(9000, 256, 64, 6), (8192, 128, 48, 8), (20000, 2048, 64, 6),
                                      (3000, 256, 72, 6), (2100, 64, 256, 8), (70, 128, 200, 40)])
 def test_routing_lds_weight_paths(ops, T, H, E, K):
