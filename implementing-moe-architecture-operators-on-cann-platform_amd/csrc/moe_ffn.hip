@@ -21,7 +21,12 @@ namespace {
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
-constexpr int64_t kTiledMinRowsPerExpert = 64;
+// Average rows per expert from which the tiled schedule runs. The streaming schedule stages at most 32 rows per
+// pass and streams an expert's weights once per pass, so it degrades once experts start to exceed 32 rows; the
+// tiled one costs about the same from 32 to 256 rows (its 256-row tiles are then mostly padding). H = 2048, E = 16,
+// K = 2, I = 8192, gate/up + down (+ permute, reduce) on one box: T = 128 (16 rows) streaming 264 / tiled 466 us;
+// T = 256 (32) 451 / 449; T = 384 (48) 541 / 458; T = 512 (64) 707 / 452; T = 1024 (128) 1271 / 480.
+constexpr int64_t kTiledMinRowsPerExpert = 32;
 
 }  // namespace
 
