@@ -21,18 +21,28 @@ namespace {
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
-// Average rows per expert from which the tiled schedule runs. The streaming schedule stages at most 32 rows per
-// pass and streams an expert's weights once per pass, so it degrades once experts start to exceed 32 rows; the
-// tiled one costs about the same from 32 to 256 rows (its 256-row tiles are then mostly padding). H = 2048, E = 16,
-// K = 2, I = 8192, gate/up + down (+ permute, reduce) on one box: T = 128 (16 rows) streaming 264 / tiled 466 us;
-// T = 256 (32) 451 / 449; T = 384 (48) 541 / 458; T = 512 (64) 707 / 452; T = 1024 (128) 1271 / 480.
+// Average rows per expert from which the tiled schedule runs. The 32-row streaming kernels stream every expert's
+// weights once per 32 rows, so they degrade once experts exceed 32 rows; the wide streaming kernels take up to 128
+// rows per pass and run in their place from 32 rows (moe_ffn_stream.hip); the tiled kernels cost about the same
+// from 32 to 256 rows (their 256-row tiles are then mostly padding). H = 2048, E = 16, K = 2, I = 8192, the FFN's
+// kernels on one box (32-row streaming / wide streaming / tiled):
+//   T = 128 (16 rows per expert)   273 / -   / 466 us
+//   T = 256 (32)                    451 / 364 / 449-493 us
+//   T = 384 (48)                    541 / 385 / 458-491 us
+//   T = 512 (64)                    707 / 440 / 452-477 us
+//   T = 768 (96)                      - / 496 / 465-482 us
+//   T = 1024 (128)                 1271 / 734 / 480-491 us
+// Shapes the wide kernels cannot run switch to the tiled schedule at 32 rows.
 constexpr int64_t kTiledMinRowsPerExpert = 32;
+constexpr int64_t kWideMaxRowsPerExpert = 80;
 
 }  // namespace
 
 int ffn_schedule(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
     const bool stream_ok = stream_supported(static_cast<int>(H), static_cast<int>(I));
-    const bool many_rows = T * K >= kTiledMinRowsPerExpert * E;
+    const int64_t limit = stream_wide_supported(static_cast<int>(H), static_cast<int>(I)) ? kWideMaxRowsPerExpert
+                                                                                          : kTiledMinRowsPerExpert;
+    const bool many_rows = T * K >= limit * E;
     if (tiled_shape_supported(H, E, I) && (many_rows || !stream_ok))
         return tiled_size_supported(T, H, K, I) ? 1 : -1;
     if (stream_ok) return 0;

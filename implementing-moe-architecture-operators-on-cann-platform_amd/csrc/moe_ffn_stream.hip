@@ -62,6 +62,8 @@ namespace {
 constexpr int kWaves = 8;                 // streaming waves per workgroup
 constexpr int kThreads = kWaves * kWave;  // 512
 constexpr int kMaxRows = 32;              // activation rows per pass (two 16-row MFMA tiles)
+constexpr int kWideRows = 128;            // wide kernel: activation rows per pass (eight 16-row MFMA tiles)
+constexpr int64_t kWideMinRows = 32;      // average rows per expert from which the wide kernel runs
 constexpr int kLdsMax = 160 * 1024 - 1024;  // gfx950 LDS per workgroup, less 1 KB for the static arrays
 
 constexpr int kTbBytes = kWaves * 2048;     // per-wave 2 KB re-layout buffers of the full-line ring
@@ -87,6 +89,7 @@ struct StreamArgs {
     int gather;                   // activation row r is x[sorted_slot[r] / K] (gate/up) or hidden[r] (down)
     const int32_t* ids;           // expert_ids [T*K]: gate/up finds each expert's rows by scanning them
     int S;                        // T*K
+    int kchunk;                   // wide kernel: K columns staged in LDS at a time (kc % kchunk == 0)
     int32_t* offsets_out;         // gate/up writes offsets [E+1] and sorted_slot [T*K] for the down kernel
     int32_t* sorted_out;
     int32_t* slot_row_out;        // and the inverse: slot_row[slot] = sorted row, for the slots of valid ids
@@ -242,6 +245,59 @@ __device__ __forceinline__ void line_pass(const StreamArgs& p, const uint16_t* l
         }
     }
     epilogue<MT, EPI>(p, acc0, acc1, off, ne, mc, n0, split, lane);
+}
+
+// Wide passes (up to kWideRows activation rows, MT row tiles): the K-range is staged in LDS one chunk of kchunk
+// columns (bpc column blocks of 64) at a time. The ring runs over the sequence of blocks chunk by chunk, each chunk
+// in the rotated order (j + rotc) % bpc, and refills each slot with the block CB places later in the sequence
+// (which may lie in the next chunk). One call multiplies the blocks of chunk c into the accumulators.
+template <int MT, int CB>
+__device__ __forceinline__ void line_chunk(const uint16_t* lds, uint16_t* tb, const uint16_t* const (&wr)[4],
+                                           f16x8 (&rg)[CB][4], f32x4 (&acc0)[MT], f32x4 (&acc1)[MT], int c,
+                                           int nchunk, int bpc, int rotc, int stride, int lane) {
+    const int row = lane & 15, kg = lane >> 4;
+    const int wrow = lane >> 3, wc = lane & 7;
+    const int nseq = nchunk * bpc;
+    for (int j0 = 0; j0 < bpc; j0 += CB) {
+#pragma unroll
+        for (int i = 0; i < CB; ++i) {
+            int jl = j0 + i + rotc;
+            jl = jl < bpc ? jl : jl - bpc;  // block of the chunk = column block of the LDS stage
+            f16x8 bf[2][2];
+#pragma unroll
+            for (int m = 0; m < 2; ++m) {
+                *reinterpret_cast<f16x8*>(tb + tb_off(wrow, wc)) = rg[i][2 * m];
+                *reinterpret_cast<f16x8*>(tb + tb_off(8 + wrow, wc)) = rg[i][2 * m + 1];
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                bf[m][0] = *reinterpret_cast<const f16x8*>(tb + tb_off(row, kg));
+                bf[m][1] = *reinterpret_cast<const f16x8*>(tb + tb_off(row, 4 + kg));
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            }
+            const int sn = c * bpc + j0 + i + CB;  // the block this slot loads next
+            if (sn < nseq) {
+                const int cn = sn / bpc;
+                int jn = sn - cn * bpc + rotc;
+                jn = jn < bpc ? jn : jn - bpc;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) rg[i][j] = load_f16x8_stream(wr[j] + (cn * bpc + jn) * 64);
+            }
+#pragma unroll
+            for (int st = 0; st < 2; ++st) {
+                f16x8 a[MT];
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+                    a[mt] = *reinterpret_cast<const f16x8*>(lds + (mt * 16 + row) * stride + (2 * jl + st) * 32 + kg * 8);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    acc0[mt] = mfma16x16x32(a[mt], bf[0][st], acc0[mt]);
+                    acc1[mt] = mfma16x16x32(a[mt], bf[1][st], acc1[mt]);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
 }
 
 // Expert e's rows by scanning ids: wave w takes the contiguous chunk w of the T*K slots.
@@ -457,6 +513,148 @@ __global__ __launch_bounds__(kThreads) void ffn_stream_kernel(StreamArgs p, int 
     }
 }
 
+// One wide pass of up to kWideRows rows: for each K chunk, every wave waits for the others to finish the previous
+// chunk, the workgroup stages the chunk's activation rows, and the active waves multiply it; the epilogue follows
+// the last chunk. The ring was primed with the first CB blocks of chunk 0.
+template <int MT, int CB, int EPI>
+__device__ __forceinline__ void wide_pass(const StreamArgs& p, uint16_t* lds, uint16_t* tb, const uint16_t* const (&wr)[4],
+                                          f16x8 (&rg)[CB][4], const int* s_rows, bool active, int rows, int rotc,
+                                          int off, int ne, int mc, int n0, int split, int lane) {
+    const int tid = static_cast<int>(threadIdx.x);
+    const int bpc = p.kchunk / 64, nchunk = p.kc / p.kchunk;
+    const int stride = p.kchunk + 8;
+    const int gpr = p.kchunk / 8;  // 16-byte granules per staged row
+    const int k0 = split * p.kc;
+    f32x4 acc0[MT], acc1[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        acc0[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        acc1[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    for (int c = 0; c < nchunk; ++c) {
+        lds_barrier();  // every wave is done with the previous chunk's rows (or the previous pass's)
+        const int total = rows * gpr;
+        for (int q0 = 0; q0 < total; q0 += 4 * kThreads) {
+            u32x4 v[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int q = q0 + t * kThreads + tid;
+                if (q < total) {
+                    const int r = q / gpr;
+                    const size_t src_row = p.gather ? static_cast<size_t>(s_rows[r] / p.K) : static_cast<size_t>(off + mc + r);
+                    v[t] = *reinterpret_cast<const u32x4*>(p.act + src_row * p.kdim + k0 + c * p.kchunk + (q % gpr) * 8);
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int q = q0 + t * kThreads + tid;
+                if (q < total) *reinterpret_cast<u32x4*>(lds + (q / gpr) * stride + (q % gpr) * 8) = v[t];
+            }
+        }
+        lds_barrier();
+        if (active) line_chunk<MT, CB>(lds, tb, wr, rg, acc0, acc1, c, nchunk, bpc, rotc, stride, lane);
+    }
+    if (active) epilogue<MT, EPI>(p, acc0, acc1, off, ne, mc, n0, split, lane);
+}
+
+// The weight-streaming schedule for up to kWideRows rows per pass (experts with ~32 to a few hundred rows): the
+// same units and full-line ring as ffn_stream_kernel, but each pass covers up to 128 rows (MT = 1, 2, 4 or 8 row
+// tiles), so an expert's weights are streamed once per 128 rows instead of once per 32, and the K-range is staged
+// in chunks of p.kchunk columns to fit 128 rows in LDS.
+template <int D, int EPI>
+__global__ __launch_bounds__(kThreads) void ffn_stream_wide_kernel(StreamArgs p, int units_per_wg) {
+    extern __shared__ __align__(16) uint16_t lds[];
+    __shared__ int s_eq[kWaves], s_lt[kWaves];
+    __shared__ int s_rows[kWideRows];
+    constexpr int CB = D / 2;
+    static_assert(CB >= 1, "the wide kernel runs the full-line ring");
+    const int wave = static_cast<int>(threadIdx.x) / kWave;
+    const int lane = lane_id();
+    const int tid = static_cast<int>(threadIdx.x);
+    const int cols_per_wave = EPI == kSwiGLU ? 16 : 32;
+    const int groups = (p.ndim + kWaves * cols_per_wave - 1) / (kWaves * cols_per_wave);
+    const int total_units = p.E * p.nsplit * groups;
+    const int u_begin = static_cast<int>(blockIdx.x) * units_per_wg;
+    const int u_end = min(u_begin + units_per_wg, total_units);
+    const int nblk = p.kc / 64;
+    const int bpc = p.kchunk / 64;
+
+    if (EPI == kSwiGLU) {
+        const int per = (p.S + static_cast<int>(gridDim.x) - 1) / static_cast<int>(gridDim.x);
+        const int s_beg = min(p.S, static_cast<int>(blockIdx.x) * per), s_end = min(p.S, s_beg + per);
+        for (int base = s_beg; base < s_end; base += 4 * kThreads) {
+            int id[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int sl = base + t * kThreads + tid;
+                id[t] = sl < s_end ? p.ids[sl] : 0;
+            }
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                if (id[t] >= 0 && id[t] < p.E) continue;
+                u32x4* dst = reinterpret_cast<u32x4*>(p.expert_out + static_cast<size_t>(base + t * kThreads + tid) * p.H);
+                for (int j = 0; j < p.H / 8; ++j) dst[j] = u32x4{0u, 0u, 0u, 0u};
+            }
+        }
+    }
+
+    int cur_e = -1, off = 0, ne = 0, before = 0;
+    for (int u = u_begin; u < u_end; ++u) {
+        const int g = u % groups;
+        const int split = (u / groups) % p.nsplit;
+        const int e = u / groups / p.nsplit;
+        if (EPI == kSwiGLU) {
+            if (e != cur_e) {
+                lds_barrier();  // every wave is done with the previous expert's counts and rows
+                expert_count(p, e, s_eq, s_lt);
+                lds_barrier();
+                off = 0;
+                ne = 0;
+                before = 0;
+#pragma unroll
+                for (int w = 0; w < kWaves; ++w) {
+                    off += s_lt[w];
+                    ne += s_eq[w];
+                    if (w < wave) before += s_eq[w];
+                }
+                cur_e = e;
+                if (g == 0 && tid == 0) {
+                    p.offsets_out[e] = off;
+                    if (e == p.E - 1) p.offsets_out[p.E] = off + ne;
+                }
+            }
+        } else {
+            off = p.offsets[e];
+            ne = p.offsets[e + 1] - off;
+        }
+        if (ne <= 0) continue;  // uniform over the workgroup
+        const int n0 = (g * kWaves + wave) * cols_per_wave;
+        const bool active = n0 < p.ndim;
+        const int k0 = split * p.kc;
+        const size_t ebase = static_cast<size_t>(e) * 3 * static_cast<size_t>(p.I) * p.H;
+        // rotated start inside each chunk, a multiple of CB (so a batch of CB blocks never wraps)
+        const int rotc = (((u * kWaves + wave) * 7 * CB) % nblk) % bpc / CB * CB;
+        const uint16_t* wbase = p.w + ebase + p.w_off + static_cast<size_t>(active ? n0 : 0) * p.kdim + k0 +
+                                static_cast<size_t>(lane >> 3) * p.kdim + (lane & 7) * 8;
+        const uint16_t* const wr[4] = {wbase, wbase + static_cast<size_t>(8) * p.kdim, wbase + p.w1_off,
+                                       wbase + p.w1_off + static_cast<size_t>(8) * p.kdim};
+        uint16_t* tb = lds + kWideRows * (p.kchunk + 8) + wave * 1024;
+        for (int mc = 0; mc < ne; mc += kWideRows) {
+            const int rows = min(kWideRows, ne - mc);
+            f16x8 rg[CB][4];
+            if (active) line_prime<CB>(wr, rotc, rg);  // the first CB blocks of chunk 0
+            if (EPI == kSwiGLU) {
+                lds_barrier();  // every wave is done reading s_rows
+                expert_rank(p, e, before, off, mc, kWideRows, s_rows, g == 0 && mc == 0 ? p.sorted_out : nullptr);
+            }
+            if (rows > 64) wide_pass<8, CB, EPI>(p, lds, tb, wr, rg, s_rows, active, rows, rotc, off, ne, mc, n0, split, lane);
+            else if (rows > 32) wide_pass<4, CB, EPI>(p, lds, tb, wr, rg, s_rows, active, rows, rotc, off, ne, mc, n0, split, lane);
+            else if (rows > 16) wide_pass<2, CB, EPI>(p, lds, tb, wr, rg, s_rows, active, rows, rotc, off, ne, mc, n0, split, lane);
+            else wide_pass<1, CB, EPI>(p, lds, tb, wr, rg, s_rows, active, rows, rotc, off, ne, mc, n0, split, lane);
+        }
+    }
+}
+
 // The split reduce's loads: the 8 columns c.. of row `row` in splits s0 .. s0 + kSplitBatch - 1, issued together
 // (split indices past the last read the last split again, always in bounds), then added into acc in split order:
 // acc = ((p0 + p1) + p2) + ... whatever the batching. The adds are selects, not branches, so the compiler cannot
@@ -628,6 +826,31 @@ hipError_t launch_stream_epi(const StreamArgs& p, int d, int units, hipStream_t 
     return err;
 }
 
+// K columns per LDS stage of the wide kernel for a K-range kc and ring depth d: the largest multiple of the ring's
+// batch (64 * d / 2 columns) dividing kc whose kWideRows rows fit the LDS beside the re-layout buffers; 0 if none.
+int wide_chunk(int kc, int d) {
+    if (d != 8 && d != 4) return 0;
+    const int step = 64 * (d / 2);
+    const int max_cols = (kLdsMax - kTbBytes) / (kWideRows * 2) - 8;
+    for (int kch = max_cols / step * step; kch >= step; kch -= step)
+        if (kc % kch == 0) return kch;
+    return 0;
+}
+
+template <int EPI>
+hipError_t launch_stream_wide(const StreamArgs& p, int d, int units, hipStream_t stream) {
+    const size_t lds = static_cast<size_t>(kWideRows) * (p.kchunk + 8) * sizeof(uint16_t) + kTbBytes;
+    const void* fn = d == 8 ? reinterpret_cast<const void*>(&ffn_stream_wide_kernel<8, EPI>)
+                            : reinterpret_cast<const void*>(&ffn_stream_wide_kernel<4, EPI>);
+    hipError_t err = ensure_lds_limit(fn, kLdsMax);
+    if (err != hipSuccess) return err;
+    const int slots = resident_workgroups(fn, kThreads, static_cast<int>(lds));
+    const int upw = slots > 0 ? (units + slots - 1) / slots : 1;
+    if (d == 8) ffn_stream_wide_kernel<8, EPI><<<(units + upw - 1) / upw, kThreads, lds, stream>>>(p, upw);
+    else ffn_stream_wide_kernel<4, EPI><<<(units + upw - 1) / upw, kThreads, lds, stream>>>(p, upw);
+    return hipGetLastError();
+}
+
 // The kernel instantiation launch_stream_epi runs for ring depth d (nullptr for none).
 template <int EPI>
 const void* stream_kernel_fn(int d) {
@@ -653,6 +876,19 @@ hipError_t prepare_ffn_stream(int H, int I) {
         const hipError_t err = ensure_lds_limit(fn, kLdsMax);
         if (err != hipSuccess) return err;
     }
+    if (stream_wide_supported(H, I)) {
+        const void* wide_fns[2] = {
+            gu.d == 8 ? reinterpret_cast<const void*>(&ffn_stream_wide_kernel<8, kSwiGLU>)
+                      : reinterpret_cast<const void*>(&ffn_stream_wide_kernel<4, kSwiGLU>),
+            dn.nsplit > 1 ? (dn.d == 8 ? reinterpret_cast<const void*>(&ffn_stream_wide_kernel<8, kPartial>)
+                                       : reinterpret_cast<const void*>(&ffn_stream_wide_kernel<4, kPartial>))
+                          : (dn.d == 8 ? reinterpret_cast<const void*>(&ffn_stream_wide_kernel<8, kScatter>)
+                                       : reinterpret_cast<const void*>(&ffn_stream_wide_kernel<4, kScatter>))};
+        for (const void* fn : wide_fns) {
+            const hipError_t err = ensure_lds_limit(fn, kLdsMax);
+            if (err != hipSuccess) return err;
+        }
+    }
     return hipSuccess;
 }
 
@@ -666,6 +902,17 @@ size_t stream_partial_bytes(int T, int H, int K, int I) {
 }
 
 bool stream_supported(int H, int I) { return pick_shape(H, false).kc > 0 && pick_shape(I, true).kc > 0; }
+
+// Whether the shape can run the wide kernels (both GEMMs' rings and K-ranges allow a chunked stage).
+bool stream_wide_supported(int H, int I) {
+    const StreamShape gu = pick_shape(H, false), dn = pick_shape(I, true);
+    return gu.kc > 0 && dn.kc > 0 && wide_chunk(gu.kc, gu.d) > 0 && wide_chunk(dn.kc, dn.d) > 0;
+}
+
+// The wide kernels run from kWideMinRows rows per expert on average (the 32-row passes then start to repeat).
+bool stream_wide(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
+    return T * K >= kWideMinRows * E && stream_wide_supported(static_cast<int>(H), static_cast<int>(I));
+}
 
 int stream_gateup_grid(int E, int H, int I) {
     (void)H;
@@ -706,14 +953,21 @@ hipError_t launch_ffn_stream(const uint16_t* x, const int32_t* expert_ids, const
     p.w_off = 0;
     p.w1_off = static_cast<size_t>(I) * H;
     p.gather = 1;
+    // experts with more than ~32 rows on average take the wide kernels (up to 128 rows per pass)
+    const bool wide = stream_wide(T, H, E, K, I);
+    const StreamShape dn = pick_shape(I, true);
     hipError_t err;
     {
         TraceScope trace("moe_ffn_gateup_swiglu", stream);
-        err = launch_stream_epi<kSwiGLU>(p, gu.d, stream_gateup_grid(E, H, I), stream);
+        if (wide) {
+            p.kchunk = wide_chunk(gu.kc, gu.d);
+            err = launch_stream_wide<kSwiGLU>(p, gu.d, stream_gateup_grid(E, H, I), stream);
+        } else {
+            err = launch_stream_epi<kSwiGLU>(p, gu.d, stream_gateup_grid(E, H, I), stream);
+        }
     }
     if (err != hipSuccess) return err;
     // down: activations = hidden rows, tiles = W_down rows n0..n0+15 and n0+16..n0+31
-    const StreamShape dn = pick_shape(I, true);
     p.act = ws.hidden;
     p.out = expert_out;
     p.partial = ws.partial;
@@ -727,8 +981,14 @@ hipError_t launch_ffn_stream(const uint16_t* x, const int32_t* expert_ids, const
     p.gather = 0;
     {
         TraceScope trace("moe_ffn_down", stream);
-        err = dn.nsplit > 1 ? launch_stream_epi<kPartial>(p, dn.d, stream_down_grid(E, H, I), stream)
-                            : launch_stream_epi<kScatter>(p, dn.d, stream_down_grid(E, H, I), stream);
+        if (wide) {
+            p.kchunk = wide_chunk(dn.kc, dn.d);
+            err = dn.nsplit > 1 ? launch_stream_wide<kPartial>(p, dn.d, stream_down_grid(E, H, I), stream)
+                                : launch_stream_wide<kScatter>(p, dn.d, stream_down_grid(E, H, I), stream);
+        } else {
+            err = dn.nsplit > 1 ? launch_stream_epi<kPartial>(p, dn.d, stream_down_grid(E, H, I), stream)
+                                : launch_stream_epi<kScatter>(p, dn.d, stream_down_grid(E, H, I), stream);
+        }
     }
     if (err != hipSuccess) return err;
     if (dn.nsplit <= 1) return y ? launch_combine(expert_out, weights, y, T, H, K, stream) : hipSuccess;

@@ -85,6 +85,10 @@ FfnGrid ffn_grid(int T, int H, int E, int K, int I);
 int stream_block_threads();
 int stream_rows_per_pass();
 bool stream_supported(int H, int I);
+// the wide weight-streaming kernels (up to 128 rows per pass): whether the shape allows them, and whether a call
+// of this size runs them
+bool stream_wide_supported(int H, int I);
+bool stream_wide(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I);
 hipError_t prepare_ffn_stream(int H, int I);  // kernel attributes, before the first launch of a call
 size_t stream_partial_bytes(int T, int H, int K, int I);
 int stream_gateup_grid(int E, int H, int I);

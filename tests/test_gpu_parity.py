@@ -434,6 +434,38 @@ def test_ffn_streaming_schedule_edges(ops, T, H, E, K, I, pattern):
     within(oracle.compare(eo[valid], eo_o[valid]), max_abs=1e-2, mean_abs=1e-3, cos=0.9999)
 
 
+@pytest.mark.parametrize("T,H,E,K,I,pattern", [
+    (256, 1024, 8, 2, 2048, "uniform"),  # 64 rows per expert: gate/up K in 2 chunks, down (one K-range) in 4
+    (200, 512, 8, 2, 2560, "skewed"),    # one expert 150 rows (passes of 128 + 22), down over 2 K-ranges (partials)
+    (150, 256, 4, 2, 512, "invalid"),    # 75 rows per expert, single chunks, ids outside [0, E)
+])
+def test_ffn_wide_streaming_schedule(ops, T, H, E, K, I, pattern):
+    """32 to 80 rows per expert on average: the weight-streaming schedule with the wide kernels (up to 128 rows per
+    pass, the K-range staged in chunks). offsets / sorted_slot and expert_out against the oracle on every slot."""
+    assert ffn_schedule(T, H, E, K, I) == 0
+    rng = np.random.default_rng(T + E + I)
+    x = rng.standard_normal((T, H)).astype(np.float16)
+    ew = np.concatenate([rng.standard_normal((E, 2 * I, H)) / math.sqrt(H),
+                         rng.standard_normal((E, I, H)) / math.sqrt(I)], axis=1).astype(np.float16)
+    ids = np.stack([rng.permutation(E)[:K] for _ in range(T)]).astype(np.int32)
+    if pattern == "skewed":
+        ids[:150, 0] = 3
+        ids[:150, 1] = rng.integers(4, E, 150)
+    elif pattern == "invalid":
+        ids[7, 1], ids[50, 0], ids[123, 1] = -1, E, 77
+    w = np.full((T, K), 0.5, np.float16)
+    log(f"[wide stream] {pattern}: T={T} H={H} E={E} K={K} I={I}")
+    eo_d, ws = run_ffn(ops, dev(x), dev(ids), dev(w), dev(ew), I)
+    eo = f32(host(eo_d))
+    check_permute(host(ws), ids, E)
+    valid = (ids >= 0) & (ids < E)
+    assert not eo[~valid].any()
+    eo_o = oracle.expert_ffn(f32(x), np.where(valid, ids, 0), f32(ew), I)
+    m = oracle.compare(eo[valid], eo_o[valid])
+    log(f"[wide stream] expert_out vs oracle: {m}")
+    within(m, max_abs=1e-2, mean_abs=1e-3, cos=0.9999)
+
+
 @pytest.mark.parametrize("T,H,E,K,I,split", [
     (64, 256, 8, 2, 512, 1),       # weight streaming, down in one K-range: FFN then the combine kernel
     (40, 512, 4, 2, 2560, 2),      # weight streaming, down over 2 K-ranges: the split reduce also combines
@@ -690,7 +722,7 @@ def ffn_schedule(T, H, E, K, I) -> int:
     (257, 320, 3, 2, 192),    # partial n-tiles in both GEMMs (I = 192 -> 2 x 128, H = 320 -> 2 x 256)
     (600, 128, 8, 3, 128),    # K = 3, two k-stages in both GEMMs (the shortest ring)
     (700, 192, 2, 1, 1408),   # >256 rows per expert (several m-tiles), DeepSeek's I, three k-stages
-    (8200, 128, 256, 2, 128), # E = 256: the permute re-reads expert_ids instead of its LDS byte copy
+    (10300, 128, 256, 2, 128), # E = 256: the permute re-reads expert_ids instead of its LDS byte copy
     (900, 128, 8, 2, 128),    # ids outside [0, E) through the permute's LDS byte copy (sentinel 255)
 ])
 def test_ffn_tiled_schedule_full_oracle(ops, T, H, E, K, I):
