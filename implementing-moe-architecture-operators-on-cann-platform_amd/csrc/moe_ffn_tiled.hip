@@ -73,8 +73,6 @@ constexpr int kFixRows = 16;  // tile rows per fix-up workgroup
 // 677 us + a 17 us fix-up split; at 2-2.5 rounds (T = 8192, E = 16; Mixtral T = 4096) the split saves 100-215 us.
 constexpr int kSplitMaxRounds = 4;
 
-enum Epilogue { kSwiGLU = 0, kScatter = 1 };
-
 struct TiledArgs {
     const uint16_t* act;         // x [T, H] (gate/up, gathered) or hidden [T*K, I] (down)
     const int32_t* sorted_slot;
@@ -124,6 +122,21 @@ __device__ __forceinline__ float swiglu_fast(float g, float u) {
     const float e = __builtin_amdgcn_exp2f(g * -1.4426950408889634f);
     return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
 }
+
+// The lane index read afresh. Values derived from lane_id() are loop-invariant, so the compiler computes them
+// once and keeps them live across the main loop, where the accumulators and fragments leave no room for them:
+// they are spilled, and each reload in the tile change or the epilogue waits (vmcnt) for every stage copy in
+// flight. A volatile read cannot be hoisted, so what make_plan and the epilogue derive from it is recomputed there.
+// Used by the down projection (spills 44 -> 28 and 24 -> 12 registers; on one box DeepSeek-V2-Lite down
+// 606-608 -> 568-571 us, prefill 496-499 -> 488-491 us, Mixtral 874 -> 868-869 us). Gate/up keeps lane_id(): its
+// code is unchanged, and with the fresh index it ran 0.5-1 % slower.
+__device__ __forceinline__ int lane_fresh() {
+    int v;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(v));
+    return v;
+}
+
+enum Epilogue { kSwiGLU = 0, kScatter = 1 };
 
 // Interleave pattern of one 16-MFMA phase: NR LDS reads and NV global->LDS copies are issued one after each of
 // its first MFMAs, so neither pipe waits for the other.
@@ -271,8 +284,9 @@ __global__ __launch_bounds__(kThreads) void ffn_tiled_kernel(TiledArgs p) {
     auto make_plan = [&](const TileRef& T, int buf, CopyPlan& P) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int r = (wave * 4 + j) * 8 + (lane / 8);
-            const uint32_t gq = static_cast<uint32_t>((lane % 8) ^ ((r >> 1) & 7));
+            // the down projection reads the lane index afresh (lane_fresh)
+            const int r = (wave * 4 + j) * 8 + ((EPI == kScatter ? lane_fresh() : lane) / 8);
+            const uint32_t gq = static_cast<uint32_t>(((EPI == kScatter ? lane_fresh() : lane) % 8) ^ ((r >> 1) & 7));
             if (p.gather) {
                 P.ao[j] = static_cast<uint32_t>(rowtab[buf * kBM + r] / p.K) * kbytes + gq * 16;
             } else {  // rows relative to the tile's first row
@@ -489,6 +503,7 @@ __global__ __launch_bounds__(kThreads) void ffn_tiled_kernel(TiledArgs p) {
         const int m = cur.mt * kBM + wm * 128 + row16;
         if (SPLIT && cur.part >= 0) {
             // a piece of a split tile: the raw fp32 sums of its k-range, [activation row][weight row] of the tile
+            const int lane_e = lane_fresh(), row16 = lane_e & 15, kg = lane_e >> 4;
             float* dst = p.partial + static_cast<size_t>(cur.part) * (kBM * kBN) + (wm * 128 + row16) * kBN + wn * 64 + kg * 4;
 #pragma unroll
             for (int i = 0; i < 8; ++i)
@@ -517,7 +532,8 @@ __global__ __launch_bounds__(kThreads) void ffn_tiled_kernel(TiledArgs p) {
             // L % 8 of row h * 8 + L / 8 (h = 0, 1). Stored straight from the MFMA layout (16 rows x 32 B per
             // instruction) the epilogue cost ~100 us per DeepSeek-V2-Lite down launch (T = 16384, E = 64, K = 6).
             uint8_t* stg = reinterpret_cast<uint8_t*>(lds) + tiled_epi_stage_offset(p.E) + wave * 2048;
-            const int rr = lane >> 3, gq = lane & 7;
+            const int lane_e = lane_fresh(), row16 = lane_e & 15, kg = lane_e >> 4;
+            const int rr = lane_e >> 3, gq = lane_e & 7;
             const int col = cur.nt * kBN + wn * 64 + gq * 8;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
