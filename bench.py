@@ -9,10 +9,11 @@ A step is one pass of the layer over one batch of synthetic input resident in HB
 through the C ABI of libmoe_mi355x.so on one stream, with caller-owned buffers allocated once.
 W warm-up steps, then five timed passes of K steps each, every pass between torch.cuda.synchronize() calls:
   1. eager: the three C-ABI calls per step, nothing else recorded -> `value` and `ms_per_step`;
-  2. graph replay: G layer steps (--graph-layers, default 10, as a serving loop captures a whole forward pass of
-     several MoE layers) captured once in a HIP graph, replayed untimed and then for K steps (y checked bit-exact
-     against the eager y first) -> `layer_us_graph_replay` per layer; one layer per graph ->
-     `layer_us_graph_replay_1`, which pays the ~9 us that separate consecutive graph launches once per layer;
+  2. graph replay: one layer step captured once in a HIP graph, replayed untimed and then for K steps (y checked
+     bit-exact against the eager y first) -> `layer_us_graph_replay`, which pays the ~9 us that separate
+     consecutive graph launches once per layer; G layer steps per graph (--graph-layers, default 10, as a serving
+     loop captures a whole forward pass of several MoE layers) -> `layer_us_graph_replay_g10` per layer (the key
+     names G);
   3. traced: eager again, with HIP events that the library records around each of its launches on the launch
      stream -> per-kernel average durations, from which `roofline` is computed.
   4. fused: the whole layer in one library call, moe_layer (an optional fast path: on the tiled schedule the
@@ -252,8 +253,8 @@ def main() -> int:
         g = graph_of(1)
         graph1_ms = replay_ms(g, 1)
         del g
-        progress(f"graph replay: {graph_ms * 1e3:.1f} us/layer with {G} layers per graph, "
-                 f"{graph1_ms * 1e3:.1f} us/layer with one (host clock)")
+        progress(f"graph replay: {graph1_ms * 1e3:.1f} us/layer with one layer per graph, "
+                 f"{graph_ms * 1e3:.1f} us/layer with {G} (host clock)")
     # 3) per-kernel HIP events recorded by the library on the launch stream: durations for the roofline
     with ops.kernel_trace() as kernels:
         traced_ms, _ = timed(step)
@@ -458,9 +459,8 @@ def main() -> int:
         "config": {"workload": f"{cfg.name} MoE layer T={T},H={H},E={E},K={K},I={I}", "tokens": T,
                    "hidden": H, "experts": E, "top_k": K, "intermediate": I, "active_experts": active},
         "layer_us_gpu_events": round(gpu_ms_per_step * 1e3, 2),
-        "layer_us_graph_replay": round(graph_ms * 1e3, 2) if graph_ms else None,
-        "graph_layers_per_replay": max(1, args.graph_layers) if graph_ms else None,
-        "layer_us_graph_replay_1": round(graph1_ms * 1e3, 2) if graph1_ms else None,
+        "layer_us_graph_replay": round(graph1_ms * 1e3, 2) if graph1_ms else None,
+        f"layer_us_graph_replay_g{max(1, args.graph_layers)}": round(graph_ms * 1e3, 2) if graph_ms else None,
         "layer_us_traced": round(traced_ms * 1e3, 2),
         "layer_us_fused": round(fused_ms * 1e3, 2),
         "layer_us_per_step_events": spread,

@@ -28,6 +28,10 @@
  *
  * Limits of the gfx950 kernels (MOE_ERR_UNSUPPORTED otherwise): H % 32 == 0, I % 32 == 0,
  * 1 <= K <= E <= 256, T*K < 2^31, and 16-byte aligned x, expert_weights, expert_out and y.
+ * Calls with many rows per expert (the LDS-tiled schedule, moe_expert_ffn_plan .schedule == 1) also need
+ * T*H*2 (x), 3*I*H*2 (one expert's weights) and T*K*4 (the sorted slots) below 2 GiB: the tiled kernels address
+ * them with 32-bit buffer offsets. Such calls beyond those bounds are rejected with the reason rather than run
+ * on the weight-streaming schedule, which would stream every expert's weights again for each 128 of its rows.
  */
 #ifndef MOE_OPS_H
 #define MOE_OPS_H
@@ -175,15 +179,17 @@ moe_status moe_combine_plan_for(int64_t num_tokens, int64_t hidden_size, int64_t
 moe_status moe_combine(const uint16_t* expert_out, const int32_t* expert_ids, const uint16_t* weights, uint16_t* y,
                        int64_t num_tokens, int64_t hidden_size, int64_t top_k, void* stream);
 
-/* MoeExpertFFN that allocates nothing and takes no workspace: no counterpart in the reference (whose kernel
- * always takes a caller workspace, op_kernel/moe_expert_ffn.cpp:613-621). It is for callers that cannot
- * allocate device memory: code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.
+/* MoeExpertFFN that allocates nothing and takes no workspace. It has no counterpart in the reference. It is for
+ * callers that cannot allocate device memory: code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc.
  * The workspace is a fixed per-GPU device array inside the library (64 MiB, held by every GPU the library runs
  * on until the process ends). Sizes whose workspace exceeds it return MOE_ERR_UNSUPPORTED before anything is
  * launched (e.g. T*K*I*2 > ~60 MiB; the LDS-tiled schedule
  * runs its down projection without the split leftover round here, so expert_out can differ from
  * moe_expert_ffn's in fp32 summation order on that schedule; the weight-streaming schedule is bit-identical).
  * Every call on a GPU shares that GPU's array: calls that overlap on one GPU (two streams or threads) race.
+ * The first call on each device looks up that device's array address and sets the kernels' LDS limits: make it
+ * outside graph capture (one eager call per device); later calls may be captured and replayed.
  * Arguments, errors and outputs otherwise as moe_expert_ffn. */
 moe_status moe_expert_ffn_no_alloc(const uint16_t* x, const int32_t* expert_ids, const uint16_t* weights,
                                    const uint16_t* expert_weights, uint16_t* expert_out, int64_t num_tokens,

@@ -438,23 +438,34 @@ def test_ffn_streaming_schedule_edges(ops, T, H, E, K, I, pattern):
     (256, 1024, 8, 2, 2048, "uniform"),  # 64 rows per expert: gate/up K in 2 chunks, down (one K-range) in 4
     (200, 512, 8, 2, 2560, "skewed"),    # one expert 150 rows (passes of 128 + 22), down over 2 K-ranges (partials)
     (150, 256, 4, 2, 512, "invalid"),    # 75 rows per expert, single chunks, ids outside [0, E)
+    (160, 640, 8, 2, 1024, "uniform"),   # H = 640 (a multiple of 128, not of 256): gate/up ring depth 4
+    (2048, 256, 64, 2, 512, "uniform"),  # E = 64, 64 rows per expert: the id scans over 4096 slots per expert
+    (512, 256, 64, 6, 512, "zipf"),      # E = 64, K = 6, Zipf(1.1) experts: the head expert takes several passes
+    (8192, 128, 256, 2, 256, "zipf"),    # E = 256, 64 rows per expert on average, head experts of thousands of rows
 ])
 def test_ffn_wide_streaming_schedule(ops, T, H, E, K, I, pattern):
     """32 to 80 rows per expert on average: the weight-streaming schedule with the wide kernels (up to 128 rows per
-    pass, the K-range staged in chunks). offsets / sorted_slot and expert_out against the oracle on every slot."""
+    pass, the K-range staged in chunks). offsets / sorted_slot and expert_out against the oracle on every slot,
+    so every expert's first and last sorted rows and every pass of the experts above 128 rows are checked."""
     assert ffn_schedule(T, H, E, K, I) == 0
     rng = np.random.default_rng(T + E + I)
     x = rng.standard_normal((T, H)).astype(np.float16)
     ew = np.concatenate([rng.standard_normal((E, 2 * I, H)) / math.sqrt(H),
                          rng.standard_normal((E, I, H)) / math.sqrt(I)], axis=1).astype(np.float16)
-    ids = np.stack([rng.permutation(E)[:K] for _ in range(T)]).astype(np.int32)
+    if pattern == "zipf":  # K distinct experts per token drawn with p(e) ~ (e + 1)^-1.1 (Gumbel top-K)
+        logp = -1.1 * np.log(np.arange(1, E + 1))
+        ids = np.argsort(-(logp + rng.gumbel(size=(T, E))), axis=1)[:, :K].astype(np.int32)
+    else:
+        ids = np.stack([rng.permutation(E)[:K] for _ in range(T)]).astype(np.int32)
     if pattern == "skewed":
         ids[:150, 0] = 3
         ids[:150, 1] = rng.integers(4, E, 150)
     elif pattern == "invalid":
         ids[7, 1], ids[50, 0], ids[123, 1] = -1, E, 77
     w = np.full((T, K), 0.5, np.float16)
-    log(f"[wide stream] {pattern}: T={T} H={H} E={E} K={K} I={I}")
+    counts = np.bincount(ids[(ids >= 0) & (ids < E)], minlength=E)
+    log(f"[wide stream] {pattern}: T={T} H={H} E={E} K={K} I={I}; rows per expert {counts.min()}..{counts.max()}, "
+        f"{int((counts > 128).sum())} experts above 128 rows, {int((counts == 0).sum())} empty")
     eo_d, ws = run_ffn(ops, dev(x), dev(ids), dev(w), dev(ew), I)
     eo = f32(host(eo_d))
     check_permute(host(ws), ids, E)
@@ -608,13 +619,20 @@ def test_baseline_config_sampled(ops, name):
     y_d = ops.MoeCombine(eo_d, ids_d, w_d, cfg.K)
     torch.cuda.synchronize()
 
-    # the sample: first and last sorted row of every expert, one row per leftover down tile, a spread of tokens
+    # the sample: first and last sorted row of every expert, one row of every (expert, m-tile) of the GEMMs, one
+    # row per leftover down tile, a spread of tokens
     offsets = ws_head[: 4 * (cfg.E + 1)].view(np.int32)
     sorted_slot = ws_head[((4 * (cfg.E + 1) + 255) // 256) * 256:][: 4 * cfg.slots].view(np.int32)
     rows = set()
+    bm = ffn_rows_per_tile(cfg)
+    rng = np.random.default_rng(7)
+    mtiles = 0
     for e in range(cfg.E):
         if counts[e]:
             rows.update((int(offsets[e]), int(offsets[e + 1]) - 1))
+            for m0 in range(0, int(counts[e]), bm):  # a row inside every m-tile (interior rows of the tile)
+                rows.add(int(offsets[e]) + int(rng.integers(m0, min(int(counts[e]), m0 + bm))))
+                mtiles += 1
     leftover = []
     if ffn_schedule(cfg.T, cfg.H, cfg.E, cfg.K, cfg.I) == 1:
         grid = min(torch.cuda.get_device_properties(0).multi_processor_count,
@@ -626,13 +644,14 @@ def test_baseline_config_sampled(ops, name):
     sample = np.array(sorted(tokens))
     covered = {int(e) for e in np.unique(ids[sample])}
     log(f"[{name}] oracle sample: {len(sample)} tokens; experts covered {len(covered)}/{int((counts > 0).sum())} "
-        f"(first and last sorted row of each); leftover down tiles covered {len(leftover)}")
+        f"(first and last sorted row of each); m-tiles covered {mtiles} (one row each, {bm}-row tiles); leftover "
+        f"down tiles covered {len(leftover)}")
     assert covered == {e for e in range(cfg.E) if counts[e]}
 
     ew_host = np.zeros((cfg.E, 3 * cfg.I, cfg.H), np.float32)
     for e in covered:
         ew_host[e] = f32(host(ew_d[int(e)]))
-    eo_o = oracle.expert_ffn(f32(x16[sample]), ids[sample], ew_host, cfg.I)
+    eo_o = oracle_ffn_threads(f32(x16[sample]), ids[sample], ew_host, cfg.I)
     del ew_host
     eo_s = f32(host(eo_d))[sample]
     m_eo = oracle.compare(eo_s, eo_o)
@@ -649,6 +668,35 @@ def test_baseline_config_sampled(ops, name):
     y_chk = oracle.combine(f32(host(eo_d)), f32(w)).astype(np.float16)
     assert np.array_equal(y_all.view(np.uint16), y_chk.view(np.uint16))
     assert np.isfinite(f32(y_all)).all()
+
+
+def oracle_ffn_threads(x: np.ndarray, ids: np.ndarray, ew: np.ndarray, I: int, workers: int = 8) -> np.ndarray:
+    """oracle.expert_ffn over token chunks in parallel threads (the C oracle runs outside the GIL); each token's
+    rows are the single-threaded oracle's, bit for bit."""
+    import concurrent.futures
+
+    T = x.shape[0]
+    bounds = np.linspace(0, T, min(T, workers) + 1).astype(int)
+    out = np.empty((T, ids.shape[1], x.shape[1]), np.float32)
+
+    def part(i: int) -> None:
+        b, e = int(bounds[i]), int(bounds[i + 1])
+        out[b:e] = oracle.expert_ffn(x[b:e], ids[b:e], ew, I)
+
+    with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
+        list(pool.map(part, range(len(bounds) - 1)))
+    return out
+
+
+def ffn_rows_per_tile(cfg) -> int:
+    import ctypes as C
+
+    from conftest import package
+
+    lib_mod = package()._lib
+    plan = lib_mod.FfnPlan()
+    assert lib_mod.load().moe_expert_ffn_plan(cfg.T, cfg.H, cfg.E, cfg.K, cfg.I, C.byref(plan)) == 0
+    return plan.rows_per_tile
 
 
 def tiled_down_grid(cfg) -> int:
@@ -704,6 +752,40 @@ def test_reference_target_case_seed44(ops):
     log(f"[ref seed 44] y vs reference NaiveMoE (all tokens): {m_y}")
     within(m_y)
     within(m_y, max_abs=1e-2, mean_abs=1e-3, cos=0.9999)
+
+
+def test_reference_harness_small_uniform_case(ops):
+    """The NPU harness's own accuracy case (tests/test_moe.cpp:344-515, smallCfg T=8 H=64 E=4 K=2 I=256): inputs
+    srand(42) / rand() uniform in [-1, 1], the three operators on their fp16 rounding, y compared with NaiveMoE.
+
+    The harness compares against NaiveMoE on the unrounded fp32 inputs with absolute thresholds (max abs < 0.05,
+    mean abs < 0.01, cos > 0.99; :486-490). Here |y| reaches ~156 (mean ~34), where one fp16 ulp is 0.125: the
+    fp16 rounding of the inputs alone moves the reference's own y by 0.054 max / 0.0138 mean (pinned on the CPU by
+    test_harness_small_uniform_fixture), so no fp16-input kernel can meet those two bars. Checked here:
+      ids          bit-exact against the reference routing on the fp16 inputs;
+      y vs NaiveMoE on the fp16 inputs (the kernels' own error): max abs < 2^-10 max|y| (two fp16 ulps of the
+                   largest output: hidden, expert_out and y are each rounded to fp16, 2^-11 relative) and
+                   mean abs < 2^-11 mean|y|, cos > 0.99999;
+      y vs NaiveMoE on the fp32 inputs (the harness's comparison): cos > 0.99, the bar that rounding leaves
+                   attainable; max and mean abs are logged."""
+    from conftest import GOLDEN_DIR
+
+    g = dict(np.load(GOLDEN_DIR / "harness_small_uniform.npz", allow_pickle=False))
+    T, H, E, K, I = (int(v) for v in g["dims"])
+    log(f"[harness uniform] T={T} H={H} E={E} K={K} I={I}")
+    x_d, wg_d, ew_d = dev(g["x"]), dev(g["w_gate"]), dev(g["expert_weights"])
+    ids_d, w_d = ops.MoeRoutingTopK(x_d, wg_d, K)
+    eo_d, _ = run_ffn(ops, x_d, ids_d, w_d, ew_d, I)
+    y = f32(host(ops.MoeCombine(eo_d, ids_d, w_d, K)))
+    assert np.array_equal(host(ids_d), g["expert_ids"])
+    ref16, ref32 = g["y_naive_fp16in"], g["y_naive"]
+    m16, m32 = oracle.compare(y, ref16), oracle.compare(y, ref32)
+    log(f"[harness uniform] |y| max {np.abs(ref32).max():.1f} mean {np.abs(ref32).mean():.2f}; y vs NaiveMoE on "
+        f"fp16 inputs {m16}; vs NaiveMoE on fp32 inputs (harness) {m32}")
+    assert m16["max_abs"] < 2.0**-10 * np.abs(ref16).max(), m16
+    assert m16["mean_abs"] < 2.0**-11 * np.abs(ref16).mean(), m16
+    assert m16["cos"] > 0.99999, m16
+    assert m32["cos"] > NS["cos"], m32
 
 
 def ffn_schedule(T, H, E, K, I) -> int:

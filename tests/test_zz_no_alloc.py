@@ -103,3 +103,39 @@ def test_no_alloc_rejects_sizes_past_the_scratch(ops):
     st = lib.moe_expert_ffn_no_alloc(p, p, p, p, p, T, H, E, K, I, None)
     assert st == MOE_ERR_UNSUPPORTED
     assert b"fixed scratch" in lib.moe_last_error()
+
+
+@pytest.mark.parametrize("T,H,E,K,I", [(128, 2048, 16, 2, 8192), (2048, 256, 8, 2, 512)])
+def test_no_alloc_graph_replay_matches_eager(ops, T, H, E, K, I):
+    """A captured no-alloc call, replayed three times with eager work and synchronisations between the replays:
+    every replay's expert_out equals the eager call's bit for bit. The first call on the device is made eagerly,
+    as the header asks (it looks up the scratch address and sets the kernels' LDS limits)."""
+    print(f"[no-alloc graph] T={T} H={H} E={E} K={K} I={I}", flush=True)
+    lib = ops._lib.load()
+    x, ids_d, ew = inputs(ops, T, H, E, K, I, 47)
+    w = torch.full((T, K), 0.5, dtype=torch.float16, device="cuda")
+    eager = torch.empty((T, K, H), dtype=torch.float16, device="cuda")
+    got = torch.empty((T, K, H), dtype=torch.float16, device="cuda")
+
+    def call(out, stream):
+        return lib.moe_expert_ffn_no_alloc(x.data_ptr(), ids_d.data_ptr(), w.data_ptr(), ew.data_ptr(),
+                                           out.data_ptr(), T, H, E, K, I, stream)
+
+    assert call(eager, torch.cuda.current_stream().cuda_stream) == 0, lib.moe_last_error()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        st = call(got, torch.cuda.current_stream().cuda_stream)
+    assert st == 0, lib.moe_last_error()
+    for rep in range(3):
+        got.fill_(float("nan"))
+        other = torch.empty((T // 2, K, H), dtype=torch.float16, device="cuda")  # eager work on the same scratch
+        assert lib.moe_expert_ffn_no_alloc(x.data_ptr(), ids_d.data_ptr(), w.data_ptr(), ew.data_ptr(),
+                                           other.data_ptr(), T // 2, H, E, K, I,
+                                           torch.cuda.current_stream().cuda_stream) == 0
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        same = torch.equal(got.view(torch.int16), eager.view(torch.int16))
+        print(f"[no-alloc graph] replay {rep}: bit-identical to eager {same}", flush=True)
+        assert same
