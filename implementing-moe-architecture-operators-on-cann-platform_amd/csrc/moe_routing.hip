@@ -9,10 +9,11 @@
 // in LDS and read back transposed (E % 8 == 0, 16-byte aligned w_gate), else from 8 strided 2-byte loads per
 // lane; both give the same bits.
 //   Phase 1: logits[16, E] = x[16, H] @ w_gate[H, E] on MFMA (v_mfma_f32_16x16x32_f16, fp32 accumulation;
-//            fp16 x fp16 products are exact in fp32). The H/32 k-steps are dealt round-robin to the W waves; with
-//            w_gate through LDS a wave keeps the loads of the next 2-3 k-steps in flight in register rings (at
-//            decode, H = 2048 and W = 16: 4 k-steps a wave), else it issues the loads of U k-steps per round trip;
-//            it keeps partial logits of every expert block in registers and parks them in LDS.
+//            fp16 x fp16 products are exact in fp32). The H/64 pairs of 32-wide k-steps are dealt round-robin to
+//            the W waves (at decode and prefill, H = 2048 and W = 16: two pairs a wave), so each x load covers
+//            whole 128-byte lines, re-laid through the wave's 2 KB x stage into the MFMA order; a wave issues the
+//            loads of 1-2 pairs per round trip; it keeps partial logits of every expert block in registers and
+//            parks them in LDS.
 //   Fold:    one thread per (token, expert) adds the W partials in wave order.
 //   Phase 2: one 16-lane DPP row per token for E <= 16, half a row (8 lanes) for larger E (each lane holding
 //            Epad / 16 or Epad / 8 experts; 4 or 8 tokens per wave at a time) runs the softmax, top-K and
@@ -46,10 +47,10 @@ constexpr int kSelLanes = 16;  // lanes that select one token's experts (phase 2
 // at E = 16 (one expert per lane) 8 lanes were slower (decode 5.44 against 5.28 us); 4 lanes at E = 64 took 22.8 us.
 constexpr int narrow_sel_lanes(int eb) { return eb == 1 ? 16 : 8; }
 
-// The narrow kernel runs E <= 64. The wave count fixes each token's summation order (wave w adds the k-steps
-// w, w + W, ... and the partials are folded in wave order), so it does not depend on the token blocks: a token's
-// ids and weights are the same whatever T is. 8 waves at E = 64, T = 16384 were 5 % faster (48.9 against 51.3 us)
-// but would make the bits depend on T.
+// The narrow kernel runs E <= 64. The wave count fixes each token's summation order (wave w adds the k-step pairs
+// w, w + W, ..., each pair's two k-steps in order, and the partials are folded in wave order), so it does not
+// depend on the token blocks: a token's ids and weights are the same whatever T is. 8 waves at E = 64 (two rounds
+// of loads a wave instead of four) made DeepSeek routing slower: 30.6 against 26.8 us in the layer.
 constexpr int waves_for(int eb, int /*tb*/) { return eb <= 2 ? 16 : 4; }
 // k-steps whose loads are issued together (E <= 32 runs 1024 threads: 128 VGPRs per lane; E <= 64 256), for tb
 // 16-token blocks per workgroup
@@ -64,13 +65,17 @@ int narrow_token_blocks(int T, int eb) {
     const int tb = T >= 16 * 4 * 256 ? 4 : T >= 16 * 2 * 256 ? 2 : 1;
     return eb == 4 ? min(tb, 2) : tb;
 }
-// LW: k-steps per round trip, (TB + EB) * 4 VGPRs of loads each, within the 128 (1024 threads) or 256 (256
-// threads) a lane has
-constexpr int lw_unroll(int eb, int tb) { return eb == 2 && tb == 4 ? 2 : 4; }
-// partial logits, then (lw) every wave's w_gate stage of 32 rows
+// LW: k-steps per round trip (whole pairs), (TB + EB) * 4 VGPRs of loads each, within the 128 (1024 threads) or
+// 256 (256 threads) a lane has
+constexpr int lw_unroll(int eb, int tb) { return tb == 4 ? 2 : 4; }
+// Each wave's 2 KB x stage (16 token rows x 128 B) lives in its own partial-logit rows when those hold 2 KB
+// (16 TB tokens x 16 EB experts x 4 B), which phase 1 does not use yet; else it follows the w_gate stages.
+constexpr bool narrow_xstage_in_part(int eb, int tb) { return tb * eb >= 2; }
+// partial logits, then (lw) every wave's w_gate stage of 32 rows, then (one token and expert block) the x stages
 constexpr size_t narrow_lds_bytes(int eb, int tb, bool lw) {
-    return static_cast<size_t>(waves_for(eb, tb)) * 16 * eb *
-           (tb * 16 * sizeof(float) + (lw ? 32 * sizeof(uint16_t) : 0));
+    return static_cast<size_t>(waves_for(eb, tb)) *
+           (16 * eb * (tb * 16 * sizeof(float) + (lw ? 32 * sizeof(uint16_t) : 0)) +
+            (narrow_xstage_in_part(eb, tb) ? 0 : 2048));
 }
 // the LDS path for w_gate: whole 16-byte chunks per row, an aligned base, 32-bit buffer offsets
 bool narrow_lds_weights(const void* w_gate, int H, int E) {
@@ -238,8 +243,8 @@ __device__ __forceinline__ int wstage_chunk(int r, int c) {
 // a lane and written to the wave's stage in their own row-major layout, and the B fragments (8 consecutive h of
 // one expert) come out of ds_read_tr16_b64, which hands lane i of each 16-lane group element i % 4 of the
 // 4-element rows addressed by lanes 4 j + i / 4 (j < 4). Without LW every fragment is 8 strided 2-byte global
-// loads.
-template <int EB, int TB, bool LW>
+// loads. NTX: x is loaded with the non-temporal hint (large batches, see kNtXBytes); the values are the same.
+template <int EB, int TB, bool LW, bool NTX = false>
 __global__ __launch_bounds__(waves_for(EB, TB) * kWave) void routing_topk_kernel(const uint16_t* __restrict__ x,
                                                                               const uint16_t* __restrict__ w_gate,
                                                                               int32_t* __restrict__ expert_ids,
@@ -248,7 +253,6 @@ __global__ __launch_bounds__(waves_for(EB, TB) * kWave) void routing_topk_kernel
                                                                               int32_t* __restrict__ counts,
                                                                               int32_t* __restrict__ rank) {
     constexpr int W = waves_for(EB, TB);
-    constexpr int U = unroll_for(EB, TB);
     constexpr int Epad = EB * 16;
     constexpr int NT = 16 * TB;  // tokens per workgroup
     // [W][NT tokens][Epad] fp32 partial logits (row (0, t) receives the fold); with LW then [W][32][Epad] fp16
@@ -260,12 +264,21 @@ __global__ __launch_bounds__(waves_for(EB, TB) * kWave) void routing_topk_kernel
     const int t0 = static_cast<int>(blockIdx.x) * NT;
 
     // ---- phase 1: partial logits on MFMA ----
-    const uint16_t* xrow[TB];
+    // x arrives in whole 128-byte lines: wave w owns the k-step pairs P = w, w + W, ... (k-steps 2P, 2P + 1, i.e.
+    // 64 columns = one line of each token row), and a load instruction covers 8 token rows x 128 B (lane -> row
+    // lane / 8 + 8 h, 16-byte chunk lane % 8). The wave re-lays each 16-row block through 2 KB of LDS (its own
+    // x stage: 128-byte rows, chunk c of row r at c ^ ((r >> 1) & 7)) into the MFMA A order (row, k-group). Half-line
+    // loads straight into that order (16 rows x 64 B per instruction) held a CU's outstanding requests to half the
+    // bytes: 32 MB of x took ~11 us more than no x at all, against 6.6 us for a streaming read of the same bytes.
+    const int xr = lane >> 3, xc = lane & 7;  // line loads: row (+ 8 h) and chunk of this lane
+    const uint16_t* xline[TB][2];
 #pragma unroll
-    for (int tb = 0; tb < TB; ++tb) {
-        const int tok = min(t0 + tb * 16 + row, T - 1);  // rows past T read a valid row; their results are dropped
-        xrow[tb] = x + static_cast<size_t>(tok) * H + kg * 8;
-    }
+    for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int tok = min(t0 + tb * 16 + xr + 8 * h, T - 1);  // rows past T read a valid row; results dropped
+            xline[tb][h] = x + static_cast<size_t>(tok) * H + xc * 8;
+        }
     f32x4 acc[TB][EB];
 #pragma unroll
     for (int tb = 0; tb < TB; ++tb)
@@ -273,6 +286,43 @@ __global__ __launch_bounds__(waves_for(EB, TB) * kWave) void routing_topk_kernel
         for (int b = 0; b < EB; ++b) acc[tb][b] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     const int nsteps = H / 32;
+    const int npairs = (nsteps + 1) / 2;  // an odd nsteps leaves the last pair's second k-step empty
+    // this wave's x stage: its own partial-logit rows (unused until phase 1 ends) when they hold 2 KB, else a
+    // region after the w_gate stages
+    uint8_t* xst = narrow_xstage_in_part(EB, TB)
+                       ? reinterpret_cast<uint8_t*>(part + wave * NT * Epad)
+                       : reinterpret_cast<uint8_t*>(part + W * NT * Epad) + (LW ? W * 32 * Epad * 2 : 0) + wave * 2048;
+    const int swr = (row >> 1) & 7;  // the A-fragment reads' swizzle (row = the lane's 16-row block row)
+    // x of pair P (column 64 P) into registers: 2 line loads per token block; the second k-step's chunks of a pair
+    // whose second k-step is past H read the first k-step's columns instead (in bounds) and are dropped below
+    auto load_x = [&](f16x8 (&xl)[TB][2], int P) __attribute__((always_inline)) {
+        const int col = P * 64 - (xc >= 4 && 2 * P + 1 >= nsteps ? 32 : 0);
+#pragma unroll
+        for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) xl[tb][h] = NTX ? load_f16x8_stream(xline[tb][h] + col) : load_f16x8(xline[tb][h] + col);
+    };
+    // the A fragments of both k-steps of the pair, per token block, through the x stage (zeros for a k-step past
+    // H, whatever x holds: 0 * inf would be NaN)
+    auto relayout_x = [&](const f16x8 (&xl)[TB][2], f16x8 (&a)[TB][2], bool in1) __attribute__((always_inline)) {
+#pragma unroll
+        for (int tb = 0; tb < TB; ++tb) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int r = xr + 8 * h;
+                *reinterpret_cast<f16x8*>(xst + r * 128 + ((xc ^ ((r >> 1) & 7)) << 4)) = xl[tb][h];
+            }
+            // the reads take what other lanes of this wave just wrote (LDS operations of one wave run in order)
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+            for (int st = 0; st < 2; ++st)
+                a[tb][st] = *reinterpret_cast<const f16x8*>(xst + row * 128 + (((4 * st + kg) ^ swr) << 4));
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // read before the next block's writes
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            if (!in1) a[tb][1] = f16x8{};
+        }
+    };
     // LW: this wave's stage, and each lane's chunk and fragment offsets
     uint8_t* wst = reinterpret_cast<uint8_t*>(part + W * NT * Epad) + wave * (32 * Epad * 2);
     int cpy_off[EB];     // byte offset in w_gate (relative to the k-step's first row) of the chunk this lane copies
@@ -296,87 +346,112 @@ __global__ __launch_bounds__(waves_for(EB, TB) * kWave) void routing_topk_kernel
             }
     }
     if constexpr (LW) {
-        // UL k-steps per round trip: their x fragments and w_gate chunks are all loaded into registers first (16
-        // bytes a lane each), then k-step by k-step the chunks are written to the wave's LDS stage (row-major,
-        // XOR-swizzled 16-byte chunks), read back as B fragments by ds_read_tr16_b64 and multiplied. The k-steps
-        // are added in the order s0, s0 + W, ... (Direct-to-LDS copies of the chunks were used here before: the
-        // compiler waits for every copy in flight before any LDS read, which held a round trip to 2 k-steps.)
-        constexpr int UL = lw_unroll(EB, TB);
+        // UP pairs per round trip: their x lines and w_gate chunks are all loaded into registers first (16 bytes a
+        // lane each), then pair by pair the x lines are re-laid into A fragments and k-step by k-step the w_gate
+        // chunks are written to the wave's LDS stage (row-major, XOR-swizzled 16-byte chunks), read back as B
+        // fragments by ds_read_tr16_b64 and multiplied. The k-steps add in the order 2 p0, 2 p0 + 1, 2 (p0 + W),
+        // ... (Direct-to-LDS copies of the chunks were used here before: the compiler waits for every copy in
+        // flight before any LDS read, which held a round trip to 2 k-steps.)
+        constexpr int UP = lw_unroll(EB, TB) / 2;
         const uint8_t* wbytes = reinterpret_cast<const uint8_t*>(w_gate);
-        // FULL: all UL k-steps of the round exist; the last round of a wave may run past H, and its extra k-steps
-        // load k-step 0 and multiply zeros (every step runs, so no load is moved behind a branch)
-        auto round = [&](int s0, auto full) __attribute__((always_inline)) {
+        // FULL: all UP pairs of the round exist; the last round of a wave may run past H, and its extra pairs
+        // load pair 0 and multiply zeros (every step runs, so no load is moved behind a branch)
+        auto round = [&](int p0, auto full) __attribute__((always_inline)) {
             constexpr bool FULL = decltype(full)::value;
-            f16x8 a[UL][TB];
-            u32x4 wv[UL][EB];
+            f16x8 xl[UP][TB][2];
+            u32x4 wv[UP][2][EB];
 #pragma unroll
-            for (int u = 0; u < UL; ++u) {
-                const int s = s0 + u * W;
-                const int k0 = (FULL || s < nsteps ? s : 0) * 32;
+            for (int v = 0; v < UP; ++v) {
+                const int P = p0 + v * W;
+                const int Pc = FULL || P < npairs ? P : 0;
+                load_x(xl[v], Pc);
 #pragma unroll
-                for (int tb = 0; tb < TB; ++tb) a[u][tb] = load_f16x8(xrow[tb] + k0);
+                for (int st = 0; st < 2; ++st) {
+                    const int k0 = min(2 * Pc + st, nsteps - 1) * 32;
 #pragma unroll
-                for (int i = 0; i < EB; ++i)
-                    wv[u][i] = *reinterpret_cast<const u32x4*>(wbytes + static_cast<size_t>(k0) * E * 2 + cpy_off[i]);
+                    for (int i = 0; i < EB; ++i)
+                        wv[v][st][i] = *reinterpret_cast<const u32x4*>(wbytes + static_cast<size_t>(k0) * E * 2 + cpy_off[i]);
+                }
             }
-            __builtin_amdgcn_sched_barrier(0);  // all UL k-steps' loads are issued before the first is waited for
+            __builtin_amdgcn_sched_barrier(0);  // all UP pairs' loads are issued before the first is waited for
 #pragma unroll
-            for (int u = 0; u < UL; ++u) {
-                const bool in = FULL || s0 + u * W < nsteps;
+            for (int v = 0; v < UP; ++v) {
+                const int P = p0 + v * W;
+                const bool in0 = FULL || P < npairs, in1 = in0 && 2 * P + 1 < nsteps;
+                f16x8 a[TB][2];
+                relayout_x(xl[v], a, in1);
+                if (!in0) {  // a pair past H contributes nothing, whatever x holds
 #pragma unroll
-                for (int i = 0; i < EB; ++i) *reinterpret_cast<u32x4*>(wst + i * 1024 + lane * 16) = wv[u][i];
-                f16x8 bv[EB];
-#pragma unroll
-                for (int b = 0; b < EB; ++b) {
-                    const s16x4 lo = lds_read_tr16(wst + frag_off[0][b]);
-                    const s16x4 hi = lds_read_tr16(wst + frag_off[1][b]);
-                    bv[b] = in ? __builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7))
-                               : f16x8{};
+                    for (int tb = 0; tb < TB; ++tb) a[tb][0] = f16x8{};
                 }
 #pragma unroll
-                for (int tb = 0; tb < TB; ++tb)
+                for (int st = 0; st < 2; ++st) {
+                    const bool in = st == 0 ? in0 : in1;
 #pragma unroll
-                    for (int b = 0; b < EB; ++b) acc[tb][b] = mfma16x16x32(a[u][tb], bv[b], acc[tb][b]);
+                    for (int i = 0; i < EB; ++i) *reinterpret_cast<u32x4*>(wst + i * 1024 + lane * 16) = wv[v][st][i];
+                    f16x8 bv[EB];
+#pragma unroll
+                    for (int b = 0; b < EB; ++b) {
+                        const s16x4 lo = lds_read_tr16(wst + frag_off[0][b]);
+                        const s16x4 hi = lds_read_tr16(wst + frag_off[1][b]);
+                        bv[b] = in ? __builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7))
+                                   : f16x8{};
+                    }
+#pragma unroll
+                    for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+                        for (int b = 0; b < EB; ++b) acc[tb][b] = mfma16x16x32(a[tb][st], bv[b], acc[tb][b]);
+                }
             }
         };
-        int s0 = wave;
-        for (; s0 + (UL - 1) * W < nsteps; s0 += UL * W) round(s0, std::true_type{});
-        if (s0 < nsteps) round(s0, std::false_type{});
-    } else {  // w_gate B fragments as 8 strided 2-byte loads each, U k-steps per round trip
-        for (int s0 = wave; s0 < nsteps; s0 += U * W) {
-            f16x8 a[U][TB];
-            f16x8 bv[U][EB];
+        int p0 = wave;
+        for (; p0 + (UP - 1) * W < npairs; p0 += UP * W) round(p0, std::true_type{});
+        if (p0 < npairs) round(p0, std::false_type{});
+    } else {  // w_gate B fragments as 8 strided 2-byte loads each, UP pairs per round trip
+        constexpr int UP = unroll_for(EB, TB) >= 2 ? unroll_for(EB, TB) / 2 : 1;
+        for (int p0 = wave; p0 < npairs; p0 += UP * W) {
+            f16x8 xl[UP][TB][2];
+            f16x8 bv[UP][2][EB];
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int s = s0 + u * W;
-                const bool in = s < nsteps;
-                const int k0 = (in ? s : 0) * 32;
+            for (int v = 0; v < UP; ++v) {
+                const int P = p0 + v * W;
+                const int Pc = P < npairs ? P : 0;
+                load_x(xl[v], Pc);
 #pragma unroll
-                for (int tb = 0; tb < TB; ++tb) {
-                    a[u][tb] = load_f16x8(xrow[tb] + k0);
-                    if (!in) {  // a k-step past H contributes nothing, whatever x holds (0 * inf would be NaN)
+                for (int st = 0; st < 2; ++st) {
+                    const bool in = P < npairs && 2 * P + st < nsteps;
+                    const uint16_t* wrow = w_gate + static_cast<size_t>(min(2 * Pc + st, nsteps - 1) * 32 + kg * 8) * E;
 #pragma unroll
-                        for (int q = 0; q < 8; ++q) a[u][tb][q] = static_cast<f16>(0.0f);
+                    for (int b = 0; b < EB; ++b) {
+                        const int e = b * 16 + row;
+#pragma unroll
+                        for (int q = 0; q < 8; ++q)
+                            bv[v][st][b][q] = (in && e < E) ? __builtin_bit_cast(f16, wrow[static_cast<size_t>(q) * E + e])
+                                                            : static_cast<f16>(0.0f);
                     }
-                }
-                const uint16_t* wrow = w_gate + static_cast<size_t>(k0 + kg * 8) * E;
-#pragma unroll
-                for (int b = 0; b < EB; ++b) {
-                    const int e = b * 16 + row;
-#pragma unroll
-                    for (int q = 0; q < 8; ++q)
-                        bv[u][b][q] = (in && e < E) ? __builtin_bit_cast(f16, wrow[static_cast<size_t>(q) * E + e])
-                                                    : static_cast<f16>(0.0f);
                 }
             }
 #pragma unroll
-            for (int u = 0; u < U; ++u)
+            for (int v = 0; v < UP; ++v) {
+                const int P = p0 + v * W;
+                f16x8 a[TB][2];
+                relayout_x(xl[v], a, P < npairs && 2 * P + 1 < nsteps);
+                if (!(P < npairs)) {  // a pair past H contributes nothing, whatever x holds
 #pragma unroll
-                for (int tb = 0; tb < TB; ++tb)
+                    for (int tb = 0; tb < TB; ++tb) a[tb][0] = f16x8{};
+                }
 #pragma unroll
-                    for (int b = 0; b < EB; ++b) acc[tb][b] = mfma16x16x32(a[u][tb], bv[u][b], acc[tb][b]);
+                for (int st = 0; st < 2; ++st)
+#pragma unroll
+                    for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+                        for (int b = 0; b < EB; ++b) acc[tb][b] = mfma16x16x32(a[tb][st], bv[v][st][b], acc[tb][b]);
+            }
         }
     }
+    // the x stage may be this wave's partial-logit rows: every stage read is done before they are written
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     // D[token tb*16 + 4*kg + r][expert b*16 + row]
 #pragma unroll
     for (int tb = 0; tb < TB; ++tb)
@@ -703,18 +778,34 @@ hipError_t launch_wide(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, 
     return hipGetLastError();
 }
 
-template <int EB, int TB, bool LW>
-hipError_t launch_narrow(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H, int E,
-                         int K, int32_t* counts, int32_t* rank, hipStream_t stream) {
+template <int EB, int TB, bool LW, bool NTX>
+hipError_t launch_narrow_nt(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H, int E,
+                            int K, int32_t* counts, int32_t* rank, hipStream_t stream) {
     const int grid = (T + 16 * TB - 1) / (16 * TB);
     const size_t lds = narrow_lds_bytes(EB, TB, LW);
-    const hipError_t attr = ensure_lds_limit(reinterpret_cast<const void*>(&routing_topk_kernel<EB, TB, LW>),
+    const hipError_t attr = ensure_lds_limit(reinterpret_cast<const void*>(&routing_topk_kernel<EB, TB, LW, NTX>),
                                              static_cast<int>(lds));
     if (attr != hipSuccess) return attr;
     TraceScope trace("moe_routing_topk", stream);
-    routing_topk_kernel<EB, TB, LW><<<grid, waves_for(EB, TB) * kWave, lds, stream>>>(x, w_gate, ids, w, T, H, E, K,
-                                                                                    counts, rank);
+    routing_topk_kernel<EB, TB, LW, NTX><<<grid, waves_for(EB, TB) * kWave, lds, stream>>>(x, w_gate, ids, w, T, H, E,
+                                                                                         K, counts, rank);
     return hipGetLastError();
+}
+
+// x bytes from which the narrow kernel loads x non-temporally. In the layer, x has been partly evicted from the
+// 256 MB Infinity Cache by the FFN's weights and intermediate when routing reads it again: at 64 MB (T = 16384,
+// H = 2048, E = 64) the hint took routing from 26.7 to 24.7 us, at 32 MB (T = 8192, E = 16) it made it slower
+// (11.5 against 11.0 us), and at decode (0.5 MB, cache-resident) it made the layer 2 us slower.
+constexpr int64_t kNtXBytes = int64_t(48) << 20;
+
+template <int EB, int TB, bool LW>
+hipError_t launch_narrow(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H, int E,
+                         int K, int32_t* counts, int32_t* rank, hipStream_t stream) {
+    if constexpr (LW && TB >= 2) {
+        if (static_cast<int64_t>(T) * H * 2 >= kNtXBytes)
+            return launch_narrow_nt<EB, TB, LW, true>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);
+    }
+    return launch_narrow_nt<EB, TB, LW, false>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);
 }
 
 template <int EB, int TB>

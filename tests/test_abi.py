@@ -97,7 +97,8 @@ def test_plans(lib):
     assert lib.moe_routing_topk_plan(128, 2048, 16, 2, C.byref(rp)) == MOE_OK
     assert (rp.grid, rp.block, rp.tokens_per_block, rp.workspace_bytes) == (8, 1024, 16, 0)
     # 16 waves x (16 tokens x 16 experts of fp32 partials + a w_gate stage of 32 rows x 16 fp16 experts)
-    assert rp.lds_bytes == 16 * (16 * 16 * 4 + 32 * 16 * 2)
+    # 16 waves: partial logits (16 tokens x 16 experts fp32), a 32-row w_gate stage, a 2 KB x stage each
+    assert rp.lds_bytes == 16 * (16 * 16 * 4 + 32 * 16 * 2 + 2048)
     # 32 < E <= 64: 4 waves per 16 tokens, or per 2 blocks of 16 when T keeps 256 workgroups busy
     assert lib.moe_routing_topk_plan(2048, 2048, 64, 6, C.byref(rp)) == MOE_OK
     # 4 waves x (16 tokens x 64 experts of fp32 partials + a w_gate stage of 32 rows x 64 fp16 experts)
