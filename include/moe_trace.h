@@ -4,7 +4,8 @@
  * No counterpart in the reference, which times whole operator chains with host std::chrono only
  * (tests/test_moe.cpp:590-612, tests/moe_cpu_sim.cpp:629-640). When enabled, the library records a HIP event
  * pair around every kernel it launches, on the stream that kernel is launched on, and accumulates the
- * elapsed times per kernel name. Disabled by default; enabling it adds two event records per launch.
+ * elapsed times per kernel name. Disabled by default; enabling it adds two event records per launch. The
+ * events carry no system-scope fence (timing only), so recording them flushes no cache.
  * The tracer is process-global and guarded by a mutex.
  */
 #ifndef MOE_TRACE_H
