@@ -343,7 +343,9 @@ def test_routing_rows_kernel_past_2gib_of_x(ops):
 
 
 @pytest.mark.parametrize("T,H,E,K", [(9000, 256, 64, 6), (8192, 128, 48, 8), (20000, 2048, 64, 6),
-                                     (3000, 256, 72, 6), (2100, 64, 256, 8), (70, 128, 200, 40)])
+                                     (3000, 256, 72, 6), (2100, 64, 256, 8), (70, 128, 200, 40),
+                                     # 55 MB of x (non-temporal x loads), H / 32 = 33 k-steps: a ragged last pair
+                                     (26000, 1056, 16, 2)])
 def test_routing_lds_weight_paths(ops, T, H, E, K):
     """w_gate through LDS: the narrow kernel's transposing-read path (E <= 64) and the rows kernel (E > 64, each
     wave 16 tokens over all of H). ids and weights against the oracle on every token; for E <= 64 also bit for bit
