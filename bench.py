@@ -10,10 +10,11 @@ through the C ABI of libmoe_mi355x.so on one stream, with caller-owned buffers a
 W warm-up steps, then five timed passes of K steps each, every pass between torch.cuda.synchronize() calls:
   1. eager: the three C-ABI calls per step, nothing else recorded -> `value` and `ms_per_step`;
   2. graph replay: one layer step captured once in a HIP graph, replayed untimed and then for K steps (y checked
-     bit-exact against the eager y first) -> `layer_us_graph_replay`, which pays the ~9 us that separate
-     consecutive graph launches once per layer; G layer steps per graph (--graph-layers, default 10, as a serving
-     loop captures a whole forward pass of several MoE layers) -> `layer_us_graph_replay_g10` per layer (the key
-     names G);
+     bit-exact against the eager y first) -> `layer_us_graph_replay`; G layer steps per graph (--graph-layers,
+     default 10, as a serving loop captures a whole forward pass of several MoE layers) ->
+     `layer_us_graph_replay_g10` per layer (the key names G). The HIP runtime's graph packet capture is off
+     (DEBUG_CLR_GRAPH_PACKET_CAPTURE=0 unless the environment sets it; recorded as `graph_packet_capture`): with
+     it on (the runtime's default) one layer per graph replayed ~3.5 us slower than the eager launches;
   3. traced: eager again, with HIP events that the library records around each of its launches on the launch
      stream -> per-kernel average durations, from which `roofline` is computed.
   4. fused: the whole layer in one library call, moe_layer (an optional fast path: on the tiled schedule the
@@ -54,6 +55,11 @@ import pathlib
 import platform
 import sys
 import time
+
+# Read when the HIP runtime starts, so set before torch is imported. By default the runtime pre-records a captured
+# graph's kernel packets and submits them together; on MI355X one layer per graph then replayed at 270.8-271.5 us
+# against 267.1-268.3 us for the same launches made eagerly, and with it off at 267.3-268.0 us (three runs each).
+os.environ.setdefault("DEBUG_CLR_GRAPH_PACKET_CAPTURE", "0")
 
 ROOT = pathlib.Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
@@ -460,6 +466,7 @@ def main() -> int:
                    "hidden": H, "experts": E, "top_k": K, "intermediate": I, "active_experts": active},
         "layer_us_gpu_events": round(gpu_ms_per_step * 1e3, 2),
         "layer_us_graph_replay": round(graph1_ms * 1e3, 2) if graph1_ms else None,
+        "graph_packet_capture": os.environ.get("DEBUG_CLR_GRAPH_PACKET_CAPTURE"),
         f"layer_us_graph_replay_g{max(1, args.graph_layers)}": round(graph_ms * 1e3, 2) if graph_ms else None,
         "layer_us_traced": round(traced_ms * 1e3, 2),
         "layer_us_fused": round(fused_ms * 1e3, 2),
