@@ -67,7 +67,7 @@ int narrow_token_blocks(int T, int eb) {
 }
 // LW: k-steps per round trip (whole pairs), (TB + EB) * 4 VGPRs of loads each, within the 128 (1024 threads) or
 // 256 (256 threads) a lane has
-constexpr int lw_unroll(int eb, int tb) { return tb == 4 ? 2 : 4; }
+constexpr int lw_unroll(int tb) { return tb == 4 ? 2 : 4; }
 // Each wave's 2 KB x stage (16 token rows x 128 B) lives in its own partial-logit rows when those hold 2 KB
 // (16 TB tokens x 16 EB experts x 4 B), which phase 1 does not use yet; else it follows the w_gate stages.
 constexpr bool narrow_xstage_in_part(int eb, int tb) { return tb * eb >= 2; }
@@ -352,7 +352,7 @@ __global__ __launch_bounds__(waves_for(EB, TB) * kWave) void routing_topk_kernel
         // fragments by ds_read_tr16_b64 and multiplied. The k-steps add in the order 2 p0, 2 p0 + 1, 2 (p0 + W),
         // ... (Direct-to-LDS copies of the chunks were used here before: the compiler waits for every copy in
         // flight before any LDS read, which held a round trip to 2 k-steps.)
-        constexpr int UP = lw_unroll(EB, TB) / 2;
+        constexpr int UP = lw_unroll(TB) / 2;
         const uint8_t* wbytes = reinterpret_cast<const uint8_t*>(w_gate);
         // FULL: all UP pairs of the round exist; the last round of a wave may run past H, and its extra pairs
         // load pair 0 and multiply zeros (every step runs, so no load is moved behind a branch)
