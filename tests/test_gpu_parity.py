@@ -1081,6 +1081,67 @@ def test_fused_layer_matches_oracle_and_operators(ops, T, H, E, K, I, schedule):
         assert torch.equal(a, b), name
 
 
+def random_shapes(n: int, seed: int):
+    """n seeded shapes inside the library's limits (H and I multiples of 32, K <= E, T <= 3000): every other one
+    with E <= 8 so that experts get the many rows of the tiled schedule; sized so the oracle FFN over every token
+    stays near 1e9 multiply-adds each."""
+    rng = np.random.default_rng(seed)
+    shapes = []
+    while len(shapes) < n:
+        H = 32 * int(rng.integers(1, 25))
+        I = 32 * int(rng.integers(1, 25))
+        E = int(rng.integers(1, 9)) if len(shapes) % 2 == 0 else int(rng.integers(1, 97))
+        K = int(rng.integers(1, min(E, 8) + 1))
+        t_cap = max(1, min(3000, int(1e9 // (3 * K * H * I))))
+        T = int(rng.integers(1, t_cap + 1))
+        shapes.append((T, H, E, K, I))
+    return shapes
+
+
+def test_random_shape_sweep(ops):
+    """Seeded random shapes through the three operators and through moe_layer, every token checked: ids and
+    weights against the oracle's routing, expert_out against the oracle FFN of the same ids, y bit for bit against
+    the oracle's combine of that expert_out, and moe_layer equal to the three operators bit for bit. Shapes the
+    planner rejects must be rejected with MOE_ERR_UNSUPPORTED; the sweep must reach both FFN schedules."""
+    import ctypes as C
+
+    from conftest import package
+
+    lib_mod = package()._lib
+    lib = lib_mod.load()
+    seen = {0: 0, 1: 0}
+    for n, (T, H, E, K, I) in enumerate(random_shapes(24, 2026)):
+        plan = lib_mod.FfnPlan()
+        st = lib.moe_expert_ffn_plan(T, H, E, K, I, C.byref(plan))
+        if st != 0:
+            assert lib_mod.STATUS_NAMES.get(st) == "MOE_ERR_UNSUPPORTED", (T, H, E, K, I, st)
+            log(f"[sweep {n}] T={T} H={H} E={E} K={K} I={I}: unsupported ({lib.moe_last_error().decode()})")
+            continue
+        seen[plan.schedule] += 1
+        rng = np.random.default_rng(n)
+        x = rng.standard_normal((T, H)).astype(np.float16)
+        wg = (rng.standard_normal((H, E)) / math.sqrt(H)).astype(np.float16)
+        ew = np.concatenate([rng.standard_normal((E, 2 * I, H)) / math.sqrt(H),
+                             rng.standard_normal((E, I, H)) / math.sqrt(I)], axis=1).astype(np.float16)
+        x_d, wg_d, ew_d = dev(x), dev(wg), dev(ew)
+        ids_d, w_d = ops.MoeRoutingTopK(x_d, wg_d, K)
+        eo_d = ops.MoeExpertFFN(x_d, ids_d, w_d, ew_d)
+        y_d = ops.MoeCombine(eo_d, ids_d, w_d, K)
+        ids, w = host(ids_d), host(w_d)
+        log(f"[sweep {n}] T={T} H={H} E={E} K={K} I={I} schedule={plan.schedule} rows/tile={plan.rows_per_tile}")
+        check_routing(ids, w, x, wg, K, f"sweep {n}")
+        eo = f32(host(eo_d))
+        within(oracle.compare(eo, oracle_ffn_threads(f32(x), ids, f32(ew), I)), max_abs=1e-2, mean_abs=1e-3,
+               cos=0.9999)
+        y_o = oracle.combine(eo, f32(w)).astype(np.float16)
+        assert np.array_equal(host(y_d).view(np.uint16), y_o.view(np.uint16))
+        layer = ops.moe_layer(x_d, wg_d, ew_d, K)
+        for name, a, b in zip(("y", "ids", "weights", "expert_out"), layer, (y_d, ids_d, w_d, eo_d)):
+            assert torch.equal(a, b), (name, n)
+    log(f"[sweep] shapes per schedule: {seen}")
+    assert seen[0] >= 3 and seen[1] >= 3, seen
+
+
 def test_decode_uses_streaming_and_prefill_uses_tiled():
     assert ffn_schedule(128, 2048, 16, 2, 8192) == 0
     assert ffn_schedule(8192, 2048, 16, 2, 8192) == 1
