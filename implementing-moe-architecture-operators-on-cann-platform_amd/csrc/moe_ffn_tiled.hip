@@ -37,7 +37,8 @@
 //   scheduling   tiles are (expert, n-tile, m-tile) with m fastest. Workgroups are dispatched round-robin over
 //                the 8 XCDs; each XCD owns a contiguous range of tiles, so the m-tiles that share a weight tile
 //                share that XCD's L2.
-// Rows past an expert's count are clamped to its last row on load and masked on store.
+// Rows past an expert's count are clamped to its last row on load and masked on store. A reduction extent that is
+// an odd multiple of 32 ends with a half stage (KT instantiation): its upper 32 columns are cleared in LDS.
 
 #include "moe_device.h"
 #include "moe_launch.h"
@@ -166,8 +167,10 @@ struct CopyPlan {
 };
 
 // SPLIT: the leftover round may be split over k (p.split); a separate instantiation, so the kernel without it
-// keeps its register allocation at tile changes.
-template <int EPI, bool SPLIT>
+// keeps its register allocation at tile changes. KT: the reduction extent is an odd multiple of 32, so the last
+// k-stage holds 32 valid columns; its copies read on into the next row (or past the buffer, as zeros), and the
+// waves zero those granules in LDS before the stage is published.
+template <int EPI, bool SPLIT, bool KT = false>
 __global__ __launch_bounds__(kThreads) void ffn_tiled_kernel(TiledArgs p) {
     extern __shared__ __align__(16) uint16_t lds[];
     const int tid = static_cast<int>(threadIdx.x);
@@ -213,7 +216,7 @@ __global__ __launch_bounds__(kThreads) void ffn_tiled_kernel(TiledArgs p) {
     // XCD x owns tiles [x * per_xcd, (x + 1) * per_xcd) (m-tiles of one weight tile are consecutive, so they
     // share that XCD's L2), and its workgroups take them round-robin: li, li + nloc, li + 2 nloc, ...; with
     // p.split the tiles left over after the full rounds are split over k (xcd_sched).
-    const int nst = p.kdim / kBK;  // >= 2
+    const int nst = (p.kdim + kBK - 1) / kBK;  // >= 2
     const int nloc = static_cast<int>(gridDim.x) / kXcds;
     const int x = static_cast<int>(blockIdx.x) % kXcds, li = static_cast<int>(blockIdx.x) / kXcds;
     const int per_xcd = (total + kXcds - 1) / kXcds;
@@ -361,7 +364,23 @@ __global__ __launch_bounds__(kThreads) void ffn_tiled_kernel(TiledArgs p) {
     // wave's copies have landed) and frees slot q % 2 for the copies of ring stage q + 2 (stage kc of plan P).
     // After the last tile those copies repeat its last stage into the free slot and the fourth phase reads
     // fragments nobody uses.
-    auto stage = [&](int q, bool first, int kc, const CopyPlan& P) __attribute__((always_inline)) {
+    // KT: this wave's copy rows of ring stage qn, logical granules 4-7 (k 32-63 of the stage) set to zero; the lane
+    // that copied a granule clears it, after its own copies have landed (vmcnt) and before the barrier that
+    // publishes the stage (the caller's lgkmcnt(0) covers these writes)
+    auto zero_tail = [&](int qn) __attribute__((always_inline)) {
+        uint16_t* sa = lds + (qn % kNStage) * kStageHalfs;
+        uint16_t* sb = sa + kBM * kPitch;
+        const int ln = lane_fresh();
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int r = (wave * 4 + j) * 8 + ln / 8;
+            if (((ln % 8) ^ ((r >> 1) & 7)) >= 4) {
+                *reinterpret_cast<u32x4*>(sa + (wave * 4 + j) * 8 * kPitch + ln * 8) = u32x4{0u, 0u, 0u, 0u};
+                *reinterpret_cast<u32x4*>(sb + (wave * 4 + j) * 8 * kPitch + ln * 8) = u32x4{0u, 0u, 0u, 0u};
+            }
+        }
+    };
+    auto stage = [&](int q, bool first, int kc, const CopyPlan& P, bool tail_next) __attribute__((always_inline)) {
         __builtin_amdgcn_sched_barrier(0);
         mma(0, A0, Bx, first);
         rdA(q, 0, 1, A1);
@@ -377,6 +396,7 @@ __global__ __launch_bounds__(kThreads) void ffn_tiled_kernel(TiledArgs p) {
         phase_sched<4, 0>();
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // this wave's copies of ring stage q + 1
+        if (KT && tail_next) zero_tail(q + 1);
         __builtin_amdgcn_s_waitcnt(0xc07f);        // lgkmcnt(0): this wave's reads of ring stage q are done
         ring_barrier();
         copy(q + 2, kc, P);
@@ -403,7 +423,7 @@ __global__ __launch_bounds__(kThreads) void ffn_tiled_kernel(TiledArgs p) {
         return *reinterpret_cast<const f16x8*>(lds + (q % kNStage) * kStageHalfs + (kBM + wn * 64 + j * 16 + row16) * kPitch +
                                                (((kk * 4 + kg) ^ sw) * 8));
     };
-    auto stage_ring = [&](int q, bool first, int kc, const CopyPlan& P) __attribute__((always_inline)) {
+    auto stage_ring = [&](int q, bool first, int kc, const CopyPlan& P, bool tail_next) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             __builtin_amdgcn_sched_barrier(0);
@@ -423,6 +443,7 @@ __global__ __launch_bounds__(kThreads) void ffn_tiled_kernel(TiledArgs p) {
             if (i < 5) Ar[(i + 3) % 4] = rdA1(q, 1, i + 3);
             if (i == 6) {
                 __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // this wave's copies of ring stage q + 1
+                if (KT && tail_next) zero_tail(q + 1);
                 __builtin_amdgcn_s_waitcnt(0xc07f);        // lgkmcnt(0): this wave's reads of ring stage q are done
                 ring_barrier();
                 copy(q + 2, kc, P);
@@ -451,9 +472,10 @@ __global__ __launch_bounds__(kThreads) void ffn_tiled_kernel(TiledArgs p) {
         }
         __builtin_amdgcn_sched_barrier(0);
     };
-    auto run_stage = [&](int q, bool first, int kc, const CopyPlan& P) __attribute__((always_inline)) {
-        if constexpr (EPI == kScatter) stage_ring(q, first, kc, P);
-        else stage(q, first, kc, P);
+    // tail_next: ring stage q + 1 is the last k-stage (KT)
+    auto run_stage = [&](int q, bool first, int kc, const CopyPlan& P, bool tail_next) __attribute__((always_inline)) {
+        if constexpr (EPI == kScatter) stage_ring(q, first, kc, P, tail_next);
+        else stage(q, first, kc, P, tail_next);
     };
 
     CopyPlan plan;
@@ -484,18 +506,19 @@ __global__ __launch_bounds__(kThreads) void ffn_tiled_kernel(TiledArgs p) {
         const int k0 = SPLIT ? cur.k0 : 0, nk = SPLIT ? cur.nk : nst;  // nk >= 2
         const int nk0 = SPLIT ? nxt.k0 : 0;
         const int kc0 = has_next ? nk0 : k0 + nk - 1, kc1 = has_next ? nk0 + 1 : k0 + nk - 1;
+        const bool tail = KT && k0 + nk == nst;  // this item ends with the 32-column k-stage
         if (nk > 2) {
-            run_stage(q0, true, k0 + 2, plan);
-            for (int s = 1; s + 2 < nk; ++s) run_stage(q0 + s, false, k0 + s + 2, plan);
+            run_stage(q0, true, k0 + 2, plan, false);
+            for (int s = 1; s + 2 < nk; ++s) run_stage(q0 + s, false, k0 + s + 2, plan, false);
             if (has_next) make_plan(nxt, (k + 1) % 3, plan);
-            run_stage(q0 + nk - 2, false, kc0, plan);
-            run_stage(q0 + nk - 1, false, kc1, plan);
+            run_stage(q0 + nk - 2, false, kc0, plan, tail);
+            run_stage(q0 + nk - 1, false, kc1, plan, false);
         } else {  // the next tile's plan is needed before the first barrier: wait for its row table here
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
             __syncthreads();
             if (has_next) make_plan(nxt, (k + 1) % 3, plan);
-            run_stage(q0, true, kc0, plan);
-            run_stage(q0 + 1, false, kc1, plan);
+            run_stage(q0, true, kc0, plan, tail);
+            run_stage(q0 + 1, false, kc1, plan, false);
         }
 
         // ---- epilogue: acc[i][j] lane holds D[weight row 4*kg + r of block j][activation row row16 of block i],
@@ -587,7 +610,7 @@ __global__ __launch_bounds__(kFixThreads) void ffn_tiled_fixup_kernel(TiledArgs 
         for (int d = 1; d < kWave; d <<= 1) v += __shfl_xor(v, d, kWave);
         total += v;
     }
-    const XcdSched xs = xcd_sched(x, total, nloc, p.kdim / kBK, 1);
+    const XcdSched xs = xcd_sched(x, total, nloc, (p.kdim + kBK - 1) / kBK, 1);
     if (xs.S < 2 || j >= xs.L) return;
     const int t = xs.base + xs.R * nloc + j;
     // expert e with prefix(e) <= t < prefix(e) + tiles(e), prefix(e) = tiles of the experts before e
@@ -640,9 +663,9 @@ __global__ __launch_bounds__(kFixThreads) void ffn_tiled_fixup_kernel(TiledArgs 
 
 // Persistent grid: at most the workgroups the device holds at once, a multiple of the XCD count. SPLIT (the down
 // projection): with p.split set, the leftover tiles are split over k and the fix-up kernel follows.
-template <int EPI, bool SPLIT>
+template <int EPI, bool SPLIT, bool KT>
 hipError_t launch_tiled(TiledArgs p, int grid, const char* name, hipStream_t stream) {
-    const void* fn = reinterpret_cast<const void*>(&ffn_tiled_kernel<EPI, SPLIT>);
+    const void* fn = reinterpret_cast<const void*>(&ffn_tiled_kernel<EPI, SPLIT, KT>);
     const int lds = tiled_lds_bytes(p.E, EPI == kScatter);
     const int resident = resident_workgroups(fn, kThreads, lds);
     if (resident > 0 && resident < grid) grid = resident;
@@ -653,7 +676,7 @@ hipError_t launch_tiled(TiledArgs p, int grid, const char* name, hipStream_t str
     p.split = (SPLIT && p.split && resident > 0 && grid <= kMaxParts) ? 1 : 0;
     {
         TraceScope trace(name, stream);
-        ffn_tiled_kernel<EPI, SPLIT><<<grid, kThreads, lds, stream>>>(p);
+        ffn_tiled_kernel<EPI, SPLIT, KT><<<grid, kThreads, lds, stream>>>(p);
     }
     hipError_t err = hipGetLastError();
     if (err != hipSuccess || !p.split) return err;
@@ -669,7 +692,7 @@ hipError_t launch_tiled(TiledArgs p, int grid, const char* name, hipStream_t str
 // Both k extents need at least two stages (the ring runs two ahead) and the tile table must fit in the LDS left
 // over by the ring.
 bool tiled_shape_supported(int64_t H, int64_t E, int64_t I) {
-    if (H % kBK != 0 || I % kBK != 0 || H < 2 * kBK || I < 2 * kBK) return false;
+    if (H % 32 != 0 || I % 32 != 0 || H <= kBK || I <= kBK) return false;
     return tiled_lds_bytes(static_cast<int>(E), true) <= kLdsMax;
 }
 // The buffer offsets are 32-bit: gathered x rows (T*H*2 bytes), one expert's weights (3*I*H*2) and the sorted
@@ -682,9 +705,12 @@ bool tiled_supported(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
     return tiled_shape_supported(H, E, I) && tiled_size_supported(T, H, K, I);
 }
 hipError_t prepare_ffn_tiled() {
-    for (const void* fn : {reinterpret_cast<const void*>(&ffn_tiled_kernel<kSwiGLU, false>),
-                           reinterpret_cast<const void*>(&ffn_tiled_kernel<kScatter, false>),
-                           reinterpret_cast<const void*>(&ffn_tiled_kernel<kScatter, true>)}) {
+    for (const void* fn : {reinterpret_cast<const void*>(&ffn_tiled_kernel<kSwiGLU, false, false>),
+                           reinterpret_cast<const void*>(&ffn_tiled_kernel<kScatter, false, false>),
+                           reinterpret_cast<const void*>(&ffn_tiled_kernel<kScatter, true, false>),
+                           reinterpret_cast<const void*>(&ffn_tiled_kernel<kSwiGLU, false, true>),
+                           reinterpret_cast<const void*>(&ffn_tiled_kernel<kScatter, false, true>),
+                           reinterpret_cast<const void*>(&ffn_tiled_kernel<kScatter, true, true>)}) {
         const hipError_t err = ensure_lds_limit(fn, kLdsMax);
         if (err != hipSuccess) return err;
     }
@@ -697,7 +723,7 @@ int tiled_block_threads() { return kThreads; }
 // min(kMaxParts, tiled_down_grid) workgroups.
 bool tiled_down_splits(int T, int E, int K, int H, int I) {
     const int rounds = (tiled_down_grid(T, E, K, H) + kMaxParts - 1) / kMaxParts;
-    return I / kBK >= 4 && rounds <= kSplitMaxRounds;
+    return (I + kBK - 1) / kBK >= 4 && rounds <= kSplitMaxRounds;
 }
 size_t tiled_partial_bytes(int T, int H, int E, int K, int I) {
     if (!tiled_down_splits(T, E, K, H, I)) return 0;
@@ -734,8 +760,10 @@ hipError_t launch_ffn_tiled(const uint16_t* x, const uint16_t* expert_weights, u
     p.ntiles_n = (I + 127) / 128;
     p.gather = 1;
     p.partial = ws.partial;
-    const hipError_t err = launch_tiled<kSwiGLU, false>(p, tiled_gateup_grid(T, E, K, I), "moe_ffn_gateup_swiglu",
-                                                        stream);
+    // an odd multiple of 32 along the reduction runs the KT instantiation, which clears the last stage's tail
+    const hipError_t err = H % kBK != 0
+                               ? launch_tiled<kSwiGLU, false, true>(p, tiled_gateup_grid(T, E, K, I), "moe_ffn_gateup_swiglu", stream)
+                               : launch_tiled<kSwiGLU, false, false>(p, tiled_gateup_grid(T, E, K, I), "moe_ffn_gateup_swiglu", stream);
     if (err != hipSuccess) return err;
     p.act = ws.hidden;
     p.out = expert_out;
@@ -744,8 +772,13 @@ hipError_t launch_ffn_tiled(const uint16_t* x, const uint16_t* expert_weights, u
     p.ntiles_n = (H + kBN - 1) / kBN;
     p.gather = 0;
     p.split = (allow_split && tiled_down_splits(T, E, K, H, I) && ws.partial != nullptr) ? 1 : 0;
-    if (p.split) return launch_tiled<kScatter, true>(p, tiled_down_grid(T, E, K, H), "moe_ffn_down", stream);
-    return launch_tiled<kScatter, false>(p, tiled_down_grid(T, E, K, H), "moe_ffn_down", stream);
+    const int dgrid = tiled_down_grid(T, E, K, H);
+    if (I % kBK != 0) {
+        if (p.split) return launch_tiled<kScatter, true, true>(p, dgrid, "moe_ffn_down", stream);
+        return launch_tiled<kScatter, false, true>(p, dgrid, "moe_ffn_down", stream);
+    }
+    if (p.split) return launch_tiled<kScatter, true, false>(p, dgrid, "moe_ffn_down", stream);
+    return launch_tiled<kScatter, false, false>(p, dgrid, "moe_ffn_down", stream);
 }
 
 }  // namespace moe

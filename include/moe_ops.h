@@ -32,9 +32,8 @@
  * T*H*2 (x), 3*I*H*2 (one expert's weights) and T*K*4 (the sorted slots) below 2 GiB: the tiled kernels address
  * them with 32-bit buffer offsets. Such calls beyond those bounds are rejected with the reason rather than run
  * on the weight-streaming schedule, which would stream every expert's weights again for each 128 of its rows.
- * The tiled schedule needs H % 64 == 0 and I % 64 == 0; a shape that is only a multiple of 32 runs on the
- * weight-streaming schedule whatever its rows per expert: correct, but each expert's weights are streamed again
- * for every 32 of its rows.
+ * The tiled schedule also needs H > 64 and I > 64 (two k-stages of 64); an odd multiple of 32 ends with a
+ * 32-column stage.
  */
 #ifndef MOE_OPS_H
 #define MOE_OPS_H

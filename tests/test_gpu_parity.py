@@ -808,6 +808,9 @@ def ffn_schedule(T, H, E, K, I) -> int:
     (700, 192, 2, 1, 1408),   # >256 rows per expert (several m-tiles), DeepSeek's I, three k-stages
     (10300, 128, 256, 2, 128), # E = 256: the permute re-reads expert_ids instead of its LDS byte copy
     (900, 128, 8, 2, 128),    # ids outside [0, E) through the permute's LDS byte copy (sentinel 255)
+    (600, 96, 4, 2, 160),     # H and I odd multiples of 32: both GEMMs end with a 32-column k-stage
+    (700, 224, 3, 2, 192),    # gate/up's k-tail only (H = 3.5 stages)
+    (1200, 352, 4, 2, 352),   # both k-tails, down's leftover round split over k (6 stages, the last piece's tail)
 ])
 def test_ffn_tiled_schedule_full_oracle(ops, T, H, E, K, I):
     assert ffn_schedule(T, H, E, K, I) == 1
