@@ -63,6 +63,10 @@ constexpr int kWaves = 8;                 // streaming waves per workgroup
 constexpr int kThreads = kWaves * kWave;  // 512
 constexpr int kMaxRows = 32;              // activation rows per pass (two 16-row MFMA tiles)
 constexpr int kWideRows = 128;            // wide kernel: activation rows per pass (eight 16-row MFMA tiles)
+// Ring depth of the wide kernels (k-steps in flight per wave), whatever the narrow kernels use: with 8 the wide
+// gate/up kernel spilled 33 registers in its loop and ran 8-12 % slower (T = 128, H = 4096, E = 8, I = 14336:
+// 390 against 358 us; T = 512, H = 2048, E = 16, I = 8192: 281 against 251 us).
+constexpr int kWideDepth = 4;
 constexpr int64_t kWideMinRows = 32;      // average rows per expert from which the wide kernel runs
 constexpr int kLdsMax = 160 * 1024 - 1024;  // gfx950 LDS per workgroup, less 1 KB for the static arrays
 
@@ -826,11 +830,10 @@ hipError_t launch_stream_epi(const StreamArgs& p, int d, int units, hipStream_t 
     return err;
 }
 
-// K columns per LDS stage of the wide kernel for a K-range kc and ring depth d: the largest multiple of the ring's
-// batch (64 * d / 2 columns) dividing kc whose kWideRows rows fit the LDS beside the re-layout buffers; 0 if none.
-int wide_chunk(int kc, int d) {
-    if (d != 8 && d != 4) return 0;
-    const int step = 64 * (d / 2);
+// K columns per LDS stage of the wide kernel for a K-range kc: the largest multiple of the ring's batch
+// (64 * kWideDepth / 2 columns) dividing kc whose kWideRows rows fit the LDS beside the re-layout buffers; 0 if none.
+int wide_chunk(int kc) {
+    const int step = 64 * (kWideDepth / 2);
     const int max_cols = (kLdsMax - kTbBytes) / (kWideRows * 2) - 8;
     for (int kch = max_cols / step * step; kch >= step; kch -= step)
         if (kc % kch == 0) return kch;
@@ -838,16 +841,14 @@ int wide_chunk(int kc, int d) {
 }
 
 template <int EPI>
-hipError_t launch_stream_wide(const StreamArgs& p, int d, int units, hipStream_t stream) {
+hipError_t launch_stream_wide(const StreamArgs& p, int units, hipStream_t stream) {
     const size_t lds = static_cast<size_t>(kWideRows) * (p.kchunk + 8) * sizeof(uint16_t) + kTbBytes;
-    const void* fn = d == 8 ? reinterpret_cast<const void*>(&ffn_stream_wide_kernel<8, EPI>)
-                            : reinterpret_cast<const void*>(&ffn_stream_wide_kernel<4, EPI>);
+    const void* fn = reinterpret_cast<const void*>(&ffn_stream_wide_kernel<kWideDepth, EPI>);
     hipError_t err = ensure_lds_limit(fn, kLdsMax);
     if (err != hipSuccess) return err;
     const int slots = resident_workgroups(fn, kThreads, static_cast<int>(lds));
     const int upw = slots > 0 ? (units + slots - 1) / slots : 1;
-    if (d == 8) ffn_stream_wide_kernel<8, EPI><<<(units + upw - 1) / upw, kThreads, lds, stream>>>(p, upw);
-    else ffn_stream_wide_kernel<4, EPI><<<(units + upw - 1) / upw, kThreads, lds, stream>>>(p, upw);
+    ffn_stream_wide_kernel<kWideDepth, EPI><<<(units + upw - 1) / upw, kThreads, lds, stream>>>(p, upw);
     return hipGetLastError();
 }
 
@@ -878,12 +879,9 @@ hipError_t prepare_ffn_stream(int H, int I) {
     }
     if (stream_wide_supported(H, I)) {
         const void* wide_fns[2] = {
-            gu.d == 8 ? reinterpret_cast<const void*>(&ffn_stream_wide_kernel<8, kSwiGLU>)
-                      : reinterpret_cast<const void*>(&ffn_stream_wide_kernel<4, kSwiGLU>),
-            dn.nsplit > 1 ? (dn.d == 8 ? reinterpret_cast<const void*>(&ffn_stream_wide_kernel<8, kPartial>)
-                                       : reinterpret_cast<const void*>(&ffn_stream_wide_kernel<4, kPartial>))
-                          : (dn.d == 8 ? reinterpret_cast<const void*>(&ffn_stream_wide_kernel<8, kScatter>)
-                                       : reinterpret_cast<const void*>(&ffn_stream_wide_kernel<4, kScatter>))};
+            reinterpret_cast<const void*>(&ffn_stream_wide_kernel<kWideDepth, kSwiGLU>),
+            dn.nsplit > 1 ? reinterpret_cast<const void*>(&ffn_stream_wide_kernel<kWideDepth, kPartial>)
+                          : reinterpret_cast<const void*>(&ffn_stream_wide_kernel<kWideDepth, kScatter>)};
         for (const void* fn : wide_fns) {
             const hipError_t err = ensure_lds_limit(fn, kLdsMax);
             if (err != hipSuccess) return err;
@@ -906,7 +904,7 @@ bool stream_supported(int H, int I) { return pick_shape(H, false).kc > 0 && pick
 // Whether the shape can run the wide kernels (both GEMMs' rings and K-ranges allow a chunked stage).
 bool stream_wide_supported(int H, int I) {
     const StreamShape gu = pick_shape(H, false), dn = pick_shape(I, true);
-    return gu.kc > 0 && dn.kc > 0 && wide_chunk(gu.kc, gu.d) > 0 && wide_chunk(dn.kc, dn.d) > 0;
+    return gu.kc > 0 && dn.kc > 0 && wide_chunk(gu.kc) > 0 && wide_chunk(dn.kc) > 0;
 }
 
 // The wide kernels run from kWideMinRows rows per expert on average (the 32-row passes then start to repeat).
@@ -960,8 +958,8 @@ hipError_t launch_ffn_stream(const uint16_t* x, const int32_t* expert_ids, const
     {
         TraceScope trace("moe_ffn_gateup_swiglu", stream);
         if (wide) {
-            p.kchunk = wide_chunk(gu.kc, gu.d);
-            err = launch_stream_wide<kSwiGLU>(p, gu.d, stream_gateup_grid(E, H, I), stream);
+            p.kchunk = wide_chunk(gu.kc);
+            err = launch_stream_wide<kSwiGLU>(p, stream_gateup_grid(E, H, I), stream);
         } else {
             err = launch_stream_epi<kSwiGLU>(p, gu.d, stream_gateup_grid(E, H, I), stream);
         }
@@ -982,9 +980,9 @@ hipError_t launch_ffn_stream(const uint16_t* x, const int32_t* expert_ids, const
     {
         TraceScope trace("moe_ffn_down", stream);
         if (wide) {
-            p.kchunk = wide_chunk(dn.kc, dn.d);
-            err = dn.nsplit > 1 ? launch_stream_wide<kPartial>(p, dn.d, stream_down_grid(E, H, I), stream)
-                                : launch_stream_wide<kScatter>(p, dn.d, stream_down_grid(E, H, I), stream);
+            p.kchunk = wide_chunk(dn.kc);
+            err = dn.nsplit > 1 ? launch_stream_wide<kPartial>(p, stream_down_grid(E, H, I), stream)
+                                : launch_stream_wide<kScatter>(p, stream_down_grid(E, H, I), stream);
         } else {
             err = dn.nsplit > 1 ? launch_stream_epi<kPartial>(p, dn.d, stream_down_grid(E, H, I), stream)
                                 : launch_stream_epi<kScatter>(p, dn.d, stream_down_grid(E, H, I), stream);
