@@ -50,7 +50,8 @@ int ffn_schedule(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
 }
 
 // Layout (each region 256-byte aligned): offsets [E+1] i32 | sorted_slot [T*K] i32 | hidden [T*K, I] fp16, then
-// for the weight-streaming schedule: partial [nsplit, T*K, H] fp32 (when the down projection is split over K) |
+// for the weight-streaming schedule: fp32 partial sums, [nsplit, T*K, H] when the down projection is split over K
+// and [nsplit, T*K, 2*I] when the 32-row gate/up kernel splits H (the larger of the two; one serves both in turn) |
 // slot_row [T*K] i32; for the tiled schedule: the permute's scratch (rank [T*K] i32, counts [chunks, E] i32),
 // then with tiled_split up to 256 fp32 partial tiles of 256 x 256 (64 MiB; one per workgroup of the down launch)
 // for the leftover round it splits over k (none when I < 256 or when the down tiles fill more than 4 rounds).
@@ -62,7 +63,7 @@ size_t ffn_workspace_bytes(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I
     const int schedule = ffn_schedule(T, H, E, K, I);
     if (schedule == 0) {
         bytes += align_up(stream_partial_bytes(static_cast<int>(T), static_cast<int>(H), static_cast<int>(K),
-                                               static_cast<int>(I)), 256);
+                                               static_cast<int>(I), stream_wide(T, H, E, K, I)), 256);
         bytes += align_up(sizeof(int32_t) * S, 256);
     } else if (schedule == 1) {
         bytes += align_up(permute_scratch_bytes(static_cast<int>(S), static_cast<int>(E)), 256);
@@ -91,7 +92,7 @@ FfnWorkspace ffn_workspace_carve(void* base, int64_t T, int64_t H, int64_t E, in
     if (schedule == 0) {
         ws.partial = reinterpret_cast<float*>(p);
         p += align_up(stream_partial_bytes(static_cast<int>(T), static_cast<int>(H), static_cast<int>(K),
-                                           static_cast<int>(I)), 256);
+                                           static_cast<int>(I), stream_wide(T, H, E, K, I)), 256);
         ws.slot_row = reinterpret_cast<int32_t*>(p);
     } else if (schedule == 1) {
         ws.pscratch = reinterpret_cast<int32_t*>(p);
@@ -113,7 +114,7 @@ FfnGrid ffn_grid(int T, int H, int E, int K, int I) {
         g.rows_per_tile = tiled_rows_per_tile();
     } else {
         g.block_threads = stream_block_threads();
-        g.gateup_blocks = stream_gateup_grid(E, H, I);
+        g.gateup_blocks = stream_gateup_grid(E, H, I, stream_wide(T, H, E, K, I));
         g.down_blocks = stream_down_grid(E, H, I);
         g.rows_per_tile = stream_rows_per_pass();
     }

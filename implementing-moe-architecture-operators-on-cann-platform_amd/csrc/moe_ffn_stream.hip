@@ -72,7 +72,10 @@ constexpr int kLdsMax = 160 * 1024 - 1024;  // gfx950 LDS per workgroup, less 1 
 
 constexpr int kTbBytes = kWaves * 2048;     // per-wave 2 KB re-layout buffers of the full-line ring
 
-enum Epilogue { kSwiGLU = 0, kScatter = 1, kPartial = 2 };
+// kGatePartial: gate/up over one K-range of a split H, writing fp32 gate and up sums that gateup_reduce_kernel adds
+// (in split order) before the SwiGLU
+enum Epilogue { kSwiGLU = 0, kScatter = 1, kPartial = 2, kGatePartial = 3 };
+__host__ __device__ constexpr bool gate_up(int epi) { return epi == kSwiGLU || epi == kGatePartial; }
 
 struct StreamArgs {
     const uint16_t* act;          // activation rows: x [T, H] (gate/up) or hidden [T*K, I] (down)
@@ -144,6 +147,10 @@ __device__ __forceinline__ void epilogue(const StreamArgs& p, const f32x4 (&acc0
             if (EPI == kSwiGLU) {
                 const float hv = swiglu_f32(acc0[mt][j], acc1[mt][j]);
                 p.out[static_cast<size_t>(off + m) * p.ndim + n0 + row] = f32_to_f16_bits(hv);
+            } else if (EPI == kGatePartial) {
+                float* dst = p.partial + (static_cast<size_t>(split) * p.total_rows + off + m) * (2 * p.ndim) + n0 + row;
+                dst[0] = acc0[mt][j];
+                dst[p.ndim] = acc1[mt][j];
             } else if (EPI == kScatter) {
                 const size_t o = static_cast<size_t>(p.sorted_slot[off + m]) * p.ndim + n0 + row;
                 p.out[o] = f32_to_f16_bits(acc0[mt][j]);
@@ -373,7 +380,7 @@ __global__ __launch_bounds__(kThreads) void ffn_stream_kernel(StreamArgs p, int 
     const int wave = static_cast<int>(threadIdx.x) / kWave;
     const int lane = lane_id();
     const int tid = static_cast<int>(threadIdx.x);
-    const int cols_per_wave = EPI == kSwiGLU ? 16 : 32;  // gate/up: 16 rows of each matrix; down: 32 rows
+    const int cols_per_wave = gate_up(EPI) ? 16 : 32;  // gate/up: 16 rows of each matrix; down: 32 rows
     const int groups = (p.ndim + kWaves * cols_per_wave - 1) / (kWaves * cols_per_wave);
     const int total_units = p.E * p.nsplit * groups;
     const int u_begin = static_cast<int>(blockIdx.x) * units_per_wg;
@@ -383,7 +390,7 @@ __global__ __launch_bounds__(kThreads) void ffn_stream_kernel(StreamArgs p, int 
     const int gpr = p.kc / 8;
     const int stride = p.kc + 8;
 
-    if (EPI == kSwiGLU) {
+    if (gate_up(EPI)) {
         // once per call: zero the expert_out rows of ids outside [0, E) (they belong to no expert); workgroup b
         // takes slots [b * per, (b + 1) * per), 4 id loads in flight per thread
         const int per = (p.S + static_cast<int>(gridDim.x) - 1) / static_cast<int>(gridDim.x);
@@ -410,7 +417,7 @@ __global__ __launch_bounds__(kThreads) void ffn_stream_kernel(StreamArgs p, int 
         const int g = u % groups;
         const int split = (u / groups) % p.nsplit;
         const int e = u / groups / p.nsplit;
-        if (EPI == kSwiGLU) {
+        if (gate_up(EPI)) {
             if (e != cur_e) {
                 if (cur_e >= 0) lds_barrier();  // every wave is done with the previous expert's counts and rows
                 expert_count(p, e, s_eq, s_lt);
@@ -426,7 +433,7 @@ __global__ __launch_bounds__(kThreads) void ffn_stream_kernel(StreamArgs p, int 
                 }
                 cur_e = e;
                 staged_mc = -1;
-                if (g == 0 && tid == 0) {
+                if (g == 0 && split == 0 && tid == 0) {
                     p.offsets_out[e] = off;
                     if (e == p.E - 1) p.offsets_out[p.E] = off + ne;
                 }
@@ -474,9 +481,9 @@ __global__ __launch_bounds__(kThreads) void ffn_stream_kernel(StreamArgs p, int 
                 staged_e = e;
                 staged_split = split;
                 staged_mc = mc;
-                if (EPI == kSwiGLU) {
+                if (gate_up(EPI)) {
                     expert_rank(p, e, before, off, mc, p.rows_cap, s_rows,
-                                g == 0 && mc == 0 ? p.sorted_out : nullptr);
+                                g == 0 && split == 0 && mc == 0 ? p.sorted_out : nullptr);
                     lds_barrier();
                 }
                 const int total = rows * gpr;
@@ -575,7 +582,7 @@ __global__ __launch_bounds__(kThreads) void ffn_stream_wide_kernel(StreamArgs p,
     const int wave = static_cast<int>(threadIdx.x) / kWave;
     const int lane = lane_id();
     const int tid = static_cast<int>(threadIdx.x);
-    const int cols_per_wave = EPI == kSwiGLU ? 16 : 32;
+    const int cols_per_wave = gate_up(EPI) ? 16 : 32;
     const int groups = (p.ndim + kWaves * cols_per_wave - 1) / (kWaves * cols_per_wave);
     const int total_units = p.E * p.nsplit * groups;
     const int u_begin = static_cast<int>(blockIdx.x) * units_per_wg;
@@ -583,7 +590,7 @@ __global__ __launch_bounds__(kThreads) void ffn_stream_wide_kernel(StreamArgs p,
     const int nblk = p.kc / 64;
     const int bpc = p.kchunk / 64;
 
-    if (EPI == kSwiGLU) {
+    if (gate_up(EPI)) {
         const int per = (p.S + static_cast<int>(gridDim.x) - 1) / static_cast<int>(gridDim.x);
         const int s_beg = min(p.S, static_cast<int>(blockIdx.x) * per), s_end = min(p.S, s_beg + per);
         for (int base = s_beg; base < s_end; base += 4 * kThreads) {
@@ -607,7 +614,7 @@ __global__ __launch_bounds__(kThreads) void ffn_stream_wide_kernel(StreamArgs p,
         const int g = u % groups;
         const int split = (u / groups) % p.nsplit;
         const int e = u / groups / p.nsplit;
-        if (EPI == kSwiGLU) {
+        if (gate_up(EPI)) {
             if (e != cur_e) {
                 lds_barrier();  // every wave is done with the previous expert's counts and rows
                 expert_count(p, e, s_eq, s_lt);
@@ -622,7 +629,7 @@ __global__ __launch_bounds__(kThreads) void ffn_stream_wide_kernel(StreamArgs p,
                     if (w < wave) before += s_eq[w];
                 }
                 cur_e = e;
-                if (g == 0 && tid == 0) {
+                if (g == 0 && split == 0 && tid == 0) {
                     p.offsets_out[e] = off;
                     if (e == p.E - 1) p.offsets_out[p.E] = off + ne;
                 }
@@ -647,9 +654,10 @@ __global__ __launch_bounds__(kThreads) void ffn_stream_wide_kernel(StreamArgs p,
             const int rows = min(kWideRows, ne - mc);
             f16x8 rg[CB][4];
             if (active) line_prime<CB>(wr, rotc, rg);  // the first CB blocks of chunk 0
-            if (EPI == kSwiGLU) {
+            if (gate_up(EPI)) {
                 lds_barrier();  // every wave is done reading s_rows
-                expert_rank(p, e, before, off, mc, kWideRows, s_rows, g == 0 && mc == 0 ? p.sorted_out : nullptr);
+                expert_rank(p, e, before, off, mc, kWideRows, s_rows,
+                            g == 0 && split == 0 && mc == 0 ? p.sorted_out : nullptr);
             }
             if (rows > 64) wide_pass<8, CB, EPI>(p, lds, tb, wr, rg, s_rows, active, rows, rotc, off, ne, mc, n0, split, lane);
             else if (rows > 32) wide_pass<4, CB, EPI>(p, lds, tb, wr, rg, s_rows, active, rows, rotc, off, ne, mc, n0, split, lane);
@@ -719,6 +727,32 @@ __global__ __launch_bounds__(256) void down_reduce_kernel(const float* __restric
 // The slots are taken kKBatch at a time: their ids, sorted rows and weights are loaded together, then all
 // their partials (slot_row holds a row only for valid ids; the others read row 0, in bounds, and are dropped).
 constexpr int kKBatch = 2;
+// hidden[r, i] = fp16(silu(gate) * up) with gate = ((g_0 + g_1) + ...) and up likewise, added in split order from
+// the kGatePartial sums ([nsplit][total_rows][2 I] fp32: gate in columns [0, I), up in [I, 2 I)); 8 columns per
+// thread. Rows past the valid rows (ids outside [0, E)) hold no sums and are skipped.
+__global__ __launch_bounds__(256) void gateup_reduce_kernel(const float* __restrict__ partial,
+                                                            const int32_t* __restrict__ offsets, int E,
+                                                            int total_rows, int I, int nsplit,
+                                                            uint16_t* __restrict__ hidden) {
+    const int vec = I / 8;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (idx >= static_cast<int64_t>(total_rows) * vec) return;
+    const int r = static_cast<int>(idx / vec);
+    const int c = static_cast<int>(idx % vec) * 8;
+    if (r >= offsets[E]) return;
+    const size_t stride = static_cast<size_t>(total_rows) * 2 * I;
+    const size_t row_off = static_cast<size_t>(r) * 2 * I + c;
+    float g[8], u[8];
+    for (int s0 = 0; s0 < nsplit; s0 += kSplitBatch) {
+        add_split_batch(partial, stride, row_off, s0, nsplit, g);
+        add_split_batch(partial, stride, row_off + I, s0, nsplit, u);
+    }
+    f16x8 o;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = __builtin_bit_cast(_Float16, f32_to_f16_bits(swiglu_f32(g[j], u[j])));
+    *reinterpret_cast<f16x8*>(hidden + static_cast<size_t>(r) * I + c) = o;
+}
+
 __global__ __launch_bounds__(256) void reduce_combine_kernel(const float* __restrict__ partial,
                                                              const int32_t* __restrict__ slot_row,
                                                              const int32_t* __restrict__ ids,
@@ -799,12 +833,40 @@ StreamShape pick_shape(int kdim, bool allow_split) {
     return StreamShape{0, 0, 0, 0};  // no layout: the caller reports unsupported
 }
 
+// Gate/up needs the whole of H per unit for its SwiGLU. When 32 rows of the whole H do not fit the LDS (H above
+// ~2200), each unit covers one K-range of H at 32 rows instead and writes fp32 gate and up sums (kGatePartial),
+// which gateup_reduce_kernel adds before the SwiGLU: one more launch and 2 * nsplit * 4 bytes per (row, i) of
+// traffic, where the whole-H layout holds 16 rows (an expert with more rows re-streams its weights per 16 rows)
+// or none at all.
+StreamShape gateup_split_shape(int H) {
+    const int kc_max = (kLdsMax - kTbBytes) / (kMaxRows * 2) - 8;
+    for (int d = 8; d >= 1; d /= 2) {
+        int best = 0;
+        for (int kc = 32 * d; kc <= kc_max && kc <= H; kc += 32 * d)
+            if (H % kc == 0) best = kc;
+        if (best > 0) return StreamShape{best, d, kMaxRows, H / best};
+    }
+    return StreamShape{0, 0, 0, 0};
+}
+StreamShape gateup_shape(int H) {
+    const StreamShape whole = pick_shape(H, false);
+    if (whole.kc > 0 && whole.rows_cap == kMaxRows) return whole;
+    const StreamShape split = gateup_split_shape(H);
+    return split.kc > 0 ? split : whole;
+}
+// The wide kernels stage the K-range in chunks whatever its length, so their gate/up always takes the whole of H
+// (no partial sums); wide_chunk(H) == 0 (H not a multiple of 128) rules the wide kernels out.
+int wide_chunk(int kc);
+StreamShape gateup_wide_shape(int H) {
+    return wide_chunk(H) > 0 ? StreamShape{H, kWideDepth, kWideRows, 1} : StreamShape{0, 0, 0, 0};
+}
+
 template <int EPI>
 hipError_t launch_stream_epi(const StreamArgs& p, int d, int units, hipStream_t stream) {
     const size_t lds = static_cast<size_t>(p.rows_cap) * (p.kc + 8) * sizeof(uint16_t) + (d >= 2 ? kTbBytes : 0);
     hipError_t err = hipSuccess;
     // pick_shape gives the down projection (kScatter, kPartial) a ring of at most 4 k-steps
-    constexpr int kMaxDepth = EPI == kSwiGLU ? 8 : 4;
+    constexpr int kMaxDepth = gate_up(EPI) ? 8 : 4;
 #define MOE_STREAM_CASE(DEPTH)                                                                                 \
     case DEPTH: {                                                                                              \
         if constexpr (DEPTH > kMaxDepth) return hipErrorInvalidValue;                                           \
@@ -857,7 +919,7 @@ template <int EPI>
 const void* stream_kernel_fn(int d) {
     switch (d) {
         case 8:
-            if constexpr (EPI == kSwiGLU) return reinterpret_cast<const void*>(&ffn_stream_kernel<8, EPI>);
+            if constexpr (gate_up(EPI)) return reinterpret_cast<const void*>(&ffn_stream_kernel<8, EPI>);
             else return nullptr;
         case 4: return reinterpret_cast<const void*>(&ffn_stream_kernel<4, EPI>);
         case 2: return reinterpret_cast<const void*>(&ffn_stream_kernel<2, EPI>);
@@ -869,8 +931,8 @@ const void* stream_kernel_fn(int d) {
 }  // namespace
 
 hipError_t prepare_ffn_stream(int H, int I) {
-    const StreamShape gu = pick_shape(H, false), dn = pick_shape(I, true);
-    const void* fns[2] = {stream_kernel_fn<kSwiGLU>(gu.d),
+    const StreamShape gu = gateup_shape(H), dn = pick_shape(I, true);
+    const void* fns[2] = {gu.nsplit > 1 ? stream_kernel_fn<kGatePartial>(gu.d) : stream_kernel_fn<kSwiGLU>(gu.d),
                           dn.nsplit > 1 ? stream_kernel_fn<kPartial>(dn.d) : stream_kernel_fn<kScatter>(dn.d)};
     for (const void* fn : fns) {
         if (!fn) return hipErrorInvalidValue;
@@ -893,17 +955,21 @@ hipError_t prepare_ffn_stream(int H, int I) {
 int stream_block_threads() { return kThreads; }
 int stream_rows_per_pass() { return kMaxRows; }
 
-size_t stream_partial_bytes(int T, int H, int K, int I) {
-    const StreamShape s = pick_shape(I, true);
-    if (s.nsplit <= 1) return 0;
-    return static_cast<size_t>(s.nsplit) * T * K * H * sizeof(float);
+// One fp32 buffer serves both splits in turn: gate/up's sums are reduced into hidden before the down projection
+// writes its own. The wide gate/up kernel never splits H.
+size_t stream_partial_bytes(int T, int H, int K, int I, bool wide) {
+    const StreamShape gu = wide ? gateup_wide_shape(H) : gateup_shape(H), dn = pick_shape(I, true);
+    const size_t rows = static_cast<size_t>(T) * K;
+    const size_t g = gu.nsplit > 1 ? static_cast<size_t>(gu.nsplit) * rows * 2 * I * sizeof(float) : 0;
+    const size_t d = dn.nsplit > 1 ? static_cast<size_t>(dn.nsplit) * rows * H * sizeof(float) : 0;
+    return g > d ? g : d;
 }
 
-bool stream_supported(int H, int I) { return pick_shape(H, false).kc > 0 && pick_shape(I, true).kc > 0; }
+bool stream_supported(int H, int I) { return gateup_shape(H).kc > 0 && pick_shape(I, true).kc > 0; }
 
 // Whether the shape can run the wide kernels (both GEMMs' rings and K-ranges allow a chunked stage).
 bool stream_wide_supported(int H, int I) {
-    const StreamShape gu = pick_shape(H, false), dn = pick_shape(I, true);
+    const StreamShape gu = gateup_wide_shape(H), dn = pick_shape(I, true);
     return gu.kc > 0 && dn.kc > 0 && wide_chunk(gu.kc) > 0 && wide_chunk(dn.kc) > 0;
 }
 
@@ -912,9 +978,8 @@ bool stream_wide(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
     return T * K >= kWideMinRows * E && stream_wide_supported(static_cast<int>(H), static_cast<int>(I));
 }
 
-int stream_gateup_grid(int E, int H, int I) {
-    (void)H;
-    return E * ((I + kWaves * 16 - 1) / (kWaves * 16));
+int stream_gateup_grid(int E, int H, int I, bool wide) {
+    return E * ((I + kWaves * 16 - 1) / (kWaves * 16)) * (wide ? gateup_wide_shape(H) : gateup_shape(H)).nsplit;
 }
 
 int stream_down_grid(int E, int H, int I) {
@@ -939,32 +1004,44 @@ hipError_t launch_ffn_stream(const uint16_t* x, const int32_t* expert_ids, const
     p.H = H;
     p.I = I;
     p.total_rows = T * K;
-    // gate/up + SwiGLU: activations = gathered x rows, tiles = W_gate and W_up rows, out = hidden
-    const StreamShape gu = pick_shape(H, false);
+    // gate/up + SwiGLU: activations = gathered x rows, tiles = W_gate and W_up rows, out = hidden (or, with H split,
+    // fp32 partial sums reduced into hidden)
+    // experts with more than ~32 rows on average take the wide kernels (up to 128 rows per pass)
+    const bool wide = stream_wide(T, H, E, K, I);
+    const StreamShape gu = wide ? gateup_wide_shape(H) : gateup_shape(H);
     p.act = x;
     p.out = ws.hidden;
+    p.partial = ws.partial;
     p.kdim = H;
     p.ndim = I;
     p.kc = gu.kc;
     p.rows_cap = gu.rows_cap;
-    p.nsplit = 1;
+    p.nsplit = gu.nsplit;
     p.w_off = 0;
     p.w1_off = static_cast<size_t>(I) * H;
     p.gather = 1;
-    // experts with more than ~32 rows on average take the wide kernels (up to 128 rows per pass)
-    const bool wide = stream_wide(T, H, E, K, I);
     const StreamShape dn = pick_shape(I, true);
     hipError_t err;
     {
         TraceScope trace("moe_ffn_gateup_swiglu", stream);
+        const int units = stream_gateup_grid(E, H, I, wide);
         if (wide) {
             p.kchunk = wide_chunk(gu.kc);
-            err = launch_stream_wide<kSwiGLU>(p, stream_gateup_grid(E, H, I), stream);
+            err = launch_stream_wide<kSwiGLU>(p, units, stream);
         } else {
-            err = launch_stream_epi<kSwiGLU>(p, gu.d, stream_gateup_grid(E, H, I), stream);
+            err = gu.nsplit > 1 ? launch_stream_epi<kGatePartial>(p, gu.d, units, stream)
+                                : launch_stream_epi<kSwiGLU>(p, gu.d, units, stream);
         }
     }
     if (err != hipSuccess) return err;
+    if (gu.nsplit > 1) {
+        TraceScope trace("moe_ffn_gateup_reduce", stream);
+        const int64_t work = static_cast<int64_t>(T) * K * (I / 8);
+        gateup_reduce_kernel<<<static_cast<int>((work + 255) / 256), 256, 0, stream>>>(ws.partial, ws.offsets, E, T * K,
+                                                                                        I, gu.nsplit, ws.hidden);
+        err = hipGetLastError();
+        if (err != hipSuccess) return err;
+    }
     // down: activations = hidden rows, tiles = W_down rows n0..n0+15 and n0+16..n0+31
     p.act = ws.hidden;
     p.out = expert_out;

@@ -479,6 +479,57 @@ def test_ffn_wide_streaming_schedule(ops, T, H, E, K, I, pattern):
     within(m, max_abs=1e-2, mean_abs=1e-3, cos=0.9999)
 
 
+@pytest.mark.parametrize("T,H,E,K,I,pattern,nsplit", [
+    (24, 4096, 8, 2, 256, "uniform", 2),   # 32-row kernel, H in two K-ranges of 2048
+    (40, 7168, 16, 4, 128, "invalid", 4),  # DeepSeek-V3's H in four K-ranges of 1792, ids outside [0, E)
+    (100, 2816, 8, 2, 96, "skewed", 11),   # eleven K-ranges of 256; one expert 150 rows (5 passes), I tail
+    (512, 7168, 16, 2, 128, "zipf", 1),    # wide kernel (64 rows per expert): all of H in 14 stages of 512
+    (200, 5120, 8, 2, 128, "skewed", 1),   # wide kernel, 10 stages of 512; one expert 150 rows (two passes)
+])
+def test_ffn_streaming_large_hidden(ops, T, H, E, K, I, pattern, nsplit):
+    """H too large for 32 rows of x to sit in LDS whole: the 32-row gate/up kernel splits H into nsplit
+    K-ranges, each workgroup writes its range's fp32 gate and up partial sums, and a reduce kernel adds the ranges
+    in order and applies SwiGLU; the wide kernel (from 32 rows per expert) stages all of H in chunks instead. The
+    plan's gate/up grid shows the split (E x ceil(I / 128) column blocks x nsplit); offsets / sorted_slot and
+    expert_out against the oracle on every slot."""
+    import ctypes as C
+
+    from conftest import package
+
+    lib_mod = package()._lib
+    plan = lib_mod.FfnPlan()
+    assert lib_mod.load().moe_expert_ffn_plan(T, H, E, K, I, C.byref(plan)) == 0
+    assert plan.schedule == 0
+    assert plan.gateup_grid == E * ((I + 127) // 128) * nsplit
+    rng = np.random.default_rng(T + H + I)
+    x = rng.standard_normal((T, H)).astype(np.float16)
+    ew = np.concatenate([rng.standard_normal((E, 2 * I, H)) / math.sqrt(H),
+                         rng.standard_normal((E, I, H)) / math.sqrt(I)], axis=1).astype(np.float16)
+    if pattern == "zipf":  # K distinct experts per token drawn with p(e) ~ (e + 1)^-1.1 (Gumbel top-K)
+        logp = -1.1 * np.log(np.arange(1, E + 1))
+        ids = np.argsort(-(logp + rng.gumbel(size=(T, E))), axis=1)[:, :K].astype(np.int32)
+    else:
+        ids = np.stack([rng.permutation(E)[:K] for _ in range(T)]).astype(np.int32)
+    if pattern == "skewed":
+        ids[:, :] = rng.integers(1, E, (T, K))
+        ids.ravel()[:150] = 0
+    elif pattern == "invalid":
+        ids[3, 1], ids[9, 0], ids[20, 2] = -1, E, 1000
+    w = np.full((T, K), 0.5, np.float16)
+    counts = np.bincount(ids[(ids >= 0) & (ids < E)], minlength=E)
+    log(f"[large H] {pattern}: T={T} H={H} E={E} K={K} I={I} nsplit={nsplit}; rows per expert "
+        f"{counts.min()}..{counts.max()}")
+    eo_d, ws = run_ffn(ops, dev(x), dev(ids), dev(w), dev(ew), I)
+    eo = f32(host(eo_d))
+    check_permute(host(ws), ids, E)
+    valid = (ids >= 0) & (ids < E)
+    assert not eo[~valid].any()
+    eo_o = oracle_ffn_threads(f32(x), np.where(valid, ids, 0), f32(ew), I)
+    m = oracle.compare(eo[valid], eo_o[valid])
+    log(f"[large H] expert_out vs oracle: {m}")
+    within(m, max_abs=1e-2, mean_abs=1e-3, cos=0.9999)
+
+
 @pytest.mark.parametrize("T,H,E,K,I,split", [
     (64, 256, 8, 2, 512, 1),       # weight streaming, down in one K-range: FFN then the combine kernel
     (40, 512, 4, 2, 2560, 2),      # weight streaming, down over 2 K-ranges: the split reduce also combines
