@@ -32,15 +32,26 @@ size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 //   T = 512 (64)                    707 / 440 / 452-477 us
 //   T = 768 (96)                      - / 496 / 465-482 us
 //   T = 1024 (128)                 1271 / 734 / 480-491 us
+// The wide/tiled crossover moves with I: the FFN (wide / tiled, us) at 64 and 80 rows per expert on average:
+//   H = 2048, E = 16, K = 2, I = 8192     420 / 501,  445 / 496   (wide still ahead at 80 rows)
+//   H = 4096, E = 8,  K = 2, I = 14336    676 / 816,  765 / 843
+//   H = 2048, E = 64, K = 6, I = 1408     332 / 353,  350 / 333   (crossover ~72 rows)
+//   H = 4096, E = 128, K = 8, I = 1536   1160 / 1241, 1264 / 1250  (~77)
+//   H = 5120, E = 16, K = 2, I = 1536     241 / 253,  270 / 264   (~74)
+//   H = 7168, E = 256, K = 8, I = 2048   5427 / 5297 at 64 rows, 5029 / 5259 at 56  (~61)
+// so the wide kernels run to 80 rows when I >= 4096 and to 72 below.
 // Shapes the wide kernels cannot run switch to the tiled schedule at 32 rows.
 constexpr int64_t kTiledMinRowsPerExpert = 32;
 constexpr int64_t kWideMaxRowsPerExpert = 80;
+constexpr int64_t kWideMaxRowsSmallI = 72;
+constexpr int64_t kWideLargeI = 4096;
 
 }  // namespace
 
 int ffn_schedule(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
     const bool stream_ok = stream_supported(static_cast<int>(H), static_cast<int>(I));
-    const int64_t limit = stream_wide_supported(static_cast<int>(H), static_cast<int>(I)) ? kWideMaxRowsPerExpert
+    const int64_t wide_limit = I >= kWideLargeI ? kWideMaxRowsPerExpert : kWideMaxRowsSmallI;
+    const int64_t limit = stream_wide_supported(static_cast<int>(H), static_cast<int>(I)) ? wide_limit
                                                                                           : kTiledMinRowsPerExpert;
     const bool many_rows = T * K >= limit * E;
     if (tiled_shape_supported(H, E, I) && (many_rows || !stream_ok))
