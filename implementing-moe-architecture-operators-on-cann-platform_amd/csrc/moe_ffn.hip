@@ -48,8 +48,8 @@ constexpr int64_t kWideLargeI = 4096;
 
 }  // namespace
 
-int ffn_schedule(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
-    const bool stream_ok = stream_supported(static_cast<int>(H), static_cast<int>(I));
+int ffn_schedule(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I, FfnSplits splits) {
+    const bool stream_ok = stream_supported(static_cast<int>(H), static_cast<int>(I), splits.gateup);
     const int64_t wide_limit = I >= kWideLargeI ? kWideMaxRowsPerExpert : kWideMaxRowsSmallI;
     const int64_t limit = stream_wide_supported(static_cast<int>(H), static_cast<int>(I)) ? wide_limit
                                                                                           : kTiledMinRowsPerExpert;
@@ -64,21 +64,21 @@ int ffn_schedule(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
 // for the weight-streaming schedule: fp32 partial sums, [nsplit, T*K, H] when the down projection is split over K
 // and [nsplit, T*K, 2*I] when the 32-row gate/up kernel splits H (the larger of the two; one serves both in turn) |
 // slot_row [T*K] i32; for the tiled schedule: the permute's scratch (rank [T*K] i32, counts [chunks, E] i32),
-// then with tiled_split up to 256 fp32 partial tiles of 256 x 256 (64 MiB; one per workgroup of the down launch)
+// then with splits.tiled up to 256 fp32 partial tiles of 256 x 256 (64 MiB; one per workgroup of the down launch)
 // for the leftover round it splits over k (none when I < 256 or when the down tiles fill more than 4 rounds).
-size_t ffn_workspace_bytes(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I, bool tiled_split) {
+size_t ffn_workspace_bytes(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I, FfnSplits splits) {
     const size_t S = static_cast<size_t>(T) * static_cast<size_t>(K);
     size_t bytes = align_up(sizeof(int32_t) * static_cast<size_t>(E + 1), 256);
     bytes += align_up(sizeof(int32_t) * S, 256);
     bytes += align_up(sizeof(uint16_t) * S * static_cast<size_t>(I), 256);
-    const int schedule = ffn_schedule(T, H, E, K, I);
+    const int schedule = ffn_schedule(T, H, E, K, I, splits);
     if (schedule == 0) {
         bytes += align_up(stream_partial_bytes(static_cast<int>(T), static_cast<int>(H), static_cast<int>(K),
-                                               static_cast<int>(I), stream_wide(T, H, E, K, I)), 256);
+                                               static_cast<int>(I), stream_wide(T, H, E, K, I), splits.gateup), 256);
         bytes += align_up(sizeof(int32_t) * S, 256);
     } else if (schedule == 1) {
         bytes += align_up(permute_scratch_bytes(static_cast<int>(S), static_cast<int>(E)), 256);
-        if (tiled_split)
+        if (splits.tiled)
             bytes += align_up(tiled_partial_bytes(static_cast<int>(T), static_cast<int>(H), static_cast<int>(E),
                                                   static_cast<int>(K), static_cast<int>(I)), 256);
     }
@@ -86,7 +86,7 @@ size_t ffn_workspace_bytes(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I
 }
 
 FfnWorkspace ffn_workspace_carve(void* base, int64_t T, int64_t H, int64_t E, int64_t K, int64_t I,
-                                 bool tiled_split) {
+                                 FfnSplits splits) {
     const size_t S = static_cast<size_t>(T) * static_cast<size_t>(K);
     char* p = static_cast<char*>(base);
     FfnWorkspace ws;
@@ -99,16 +99,16 @@ FfnWorkspace ffn_workspace_carve(void* base, int64_t T, int64_t H, int64_t E, in
     ws.partial = nullptr;
     ws.slot_row = nullptr;
     ws.pscratch = nullptr;
-    const int schedule = ffn_schedule(T, H, E, K, I);
+    const int schedule = ffn_schedule(T, H, E, K, I, splits);
     if (schedule == 0) {
         ws.partial = reinterpret_cast<float*>(p);
         p += align_up(stream_partial_bytes(static_cast<int>(T), static_cast<int>(H), static_cast<int>(K),
-                                           static_cast<int>(I), stream_wide(T, H, E, K, I)), 256);
+                                           static_cast<int>(I), stream_wide(T, H, E, K, I), splits.gateup), 256);
         ws.slot_row = reinterpret_cast<int32_t*>(p);
     } else if (schedule == 1) {
         ws.pscratch = reinterpret_cast<int32_t*>(p);
         p += align_up(permute_scratch_bytes(static_cast<int>(S), static_cast<int>(E)), 256);
-        if (tiled_split && tiled_partial_bytes(static_cast<int>(T), static_cast<int>(H), static_cast<int>(E),
+        if (splits.tiled && tiled_partial_bytes(static_cast<int>(T), static_cast<int>(H), static_cast<int>(E),
                                                static_cast<int>(K), static_cast<int>(I)) > 0)
             ws.partial = reinterpret_cast<float*>(p);
     }
@@ -134,19 +134,20 @@ FfnGrid ffn_grid(int T, int H, int E, int K, int I) {
 
 hipError_t launch_ffn(const uint16_t* x, const int32_t* expert_ids, const uint16_t* expert_weights,
                       uint16_t* expert_out, FfnWorkspace ws, int T, int H, int E, int K, int I, hipStream_t stream,
-                      bool tiled_split) {
-    switch (ffn_schedule(T, H, E, K, I)) {
+                      FfnSplits splits) {
+    switch (ffn_schedule(T, H, E, K, I, splits)) {
         case 1: {
             hipError_t err = prepare_permute(T * K, E);
             if (err == hipSuccess) err = prepare_ffn_tiled();
             if (err == hipSuccess) err = launch_permute(expert_ids, T * K, E, H, ws, expert_out, stream);
             if (err != hipSuccess) return err;
-            return launch_ffn_tiled(x, expert_weights, expert_out, ws, T, H, E, K, I, stream, tiled_split);
+            return launch_ffn_tiled(x, expert_weights, expert_out, ws, T, H, E, K, I, stream, splits.tiled);
         }
         case 0: {
-            const hipError_t err = prepare_ffn_stream(H, I);
+            const hipError_t err = prepare_ffn_stream(H, I, splits.gateup);
             if (err != hipSuccess) return err;
-            return launch_ffn_stream(x, expert_ids, expert_weights, expert_out, ws, T, H, E, K, I, stream);
+            return launch_ffn_stream(x, expert_ids, expert_weights, expert_out, ws, T, H, E, K, I, stream, nullptr,
+                                     nullptr, splits.gateup);
         }
         default: return hipErrorInvalidValue;
     }

@@ -848,10 +848,10 @@ StreamShape gateup_split_shape(int H) {
     }
     return StreamShape{0, 0, 0, 0};
 }
-StreamShape gateup_shape(int H) {
+StreamShape gateup_shape(int H, bool allow_split) {
     const StreamShape whole = pick_shape(H, false);
     if (whole.kc > 0 && whole.rows_cap == kMaxRows) return whole;
-    const StreamShape split = gateup_split_shape(H);
+    const StreamShape split = allow_split ? gateup_split_shape(H) : StreamShape{0, 0, 0, 0};
     return split.kc > 0 ? split : whole;
 }
 // The wide kernels stage the K-range in chunks whatever its length, so their gate/up always takes the whole of H
@@ -930,8 +930,8 @@ const void* stream_kernel_fn(int d) {
 
 }  // namespace
 
-hipError_t prepare_ffn_stream(int H, int I) {
-    const StreamShape gu = gateup_shape(H), dn = pick_shape(I, true);
+hipError_t prepare_ffn_stream(int H, int I, bool gateup_split) {
+    const StreamShape gu = gateup_shape(H, gateup_split), dn = pick_shape(I, true);
     const void* fns[2] = {gu.nsplit > 1 ? stream_kernel_fn<kGatePartial>(gu.d) : stream_kernel_fn<kSwiGLU>(gu.d),
                           dn.nsplit > 1 ? stream_kernel_fn<kPartial>(dn.d) : stream_kernel_fn<kScatter>(dn.d)};
     for (const void* fn : fns) {
@@ -957,15 +957,17 @@ int stream_rows_per_pass() { return kMaxRows; }
 
 // One fp32 buffer serves both splits in turn: gate/up's sums are reduced into hidden before the down projection
 // writes its own. The wide gate/up kernel never splits H.
-size_t stream_partial_bytes(int T, int H, int K, int I, bool wide) {
-    const StreamShape gu = wide ? gateup_wide_shape(H) : gateup_shape(H), dn = pick_shape(I, true);
+size_t stream_partial_bytes(int T, int H, int K, int I, bool wide, bool gateup_split) {
+    const StreamShape gu = wide ? gateup_wide_shape(H) : gateup_shape(H, gateup_split), dn = pick_shape(I, true);
     const size_t rows = static_cast<size_t>(T) * K;
     const size_t g = gu.nsplit > 1 ? static_cast<size_t>(gu.nsplit) * rows * 2 * I * sizeof(float) : 0;
     const size_t d = dn.nsplit > 1 ? static_cast<size_t>(dn.nsplit) * rows * H * sizeof(float) : 0;
     return g > d ? g : d;
 }
 
-bool stream_supported(int H, int I) { return gateup_shape(H).kc > 0 && pick_shape(I, true).kc > 0; }
+bool stream_supported(int H, int I, bool gateup_split) {
+    return gateup_shape(H, gateup_split).kc > 0 && pick_shape(I, true).kc > 0;
+}
 
 // Whether the shape can run the wide kernels (both GEMMs' rings and K-ranges allow a chunked stage).
 bool stream_wide_supported(int H, int I) {
@@ -978,8 +980,9 @@ bool stream_wide(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
     return T * K >= kWideMinRows * E && stream_wide_supported(static_cast<int>(H), static_cast<int>(I));
 }
 
-int stream_gateup_grid(int E, int H, int I, bool wide) {
-    return E * ((I + kWaves * 16 - 1) / (kWaves * 16)) * (wide ? gateup_wide_shape(H) : gateup_shape(H)).nsplit;
+int stream_gateup_grid(int E, int H, int I, bool wide, bool gateup_split) {
+    return E * ((I + kWaves * 16 - 1) / (kWaves * 16)) *
+           (wide ? gateup_wide_shape(H) : gateup_shape(H, gateup_split)).nsplit;
 }
 
 int stream_down_grid(int E, int H, int I) {
@@ -988,7 +991,7 @@ int stream_down_grid(int E, int H, int I) {
 
 hipError_t launch_ffn_stream(const uint16_t* x, const int32_t* expert_ids, const uint16_t* expert_weights,
                              uint16_t* expert_out, const FfnWorkspace& ws, int T, int H, int E, int K, int I,
-                             hipStream_t stream, const uint16_t* weights, uint16_t* y) {
+                             hipStream_t stream, const uint16_t* weights, uint16_t* y, bool gateup_split) {
     StreamArgs p{};
     p.sorted_slot = ws.sorted_slot;
     p.ids = expert_ids;
@@ -1008,7 +1011,7 @@ hipError_t launch_ffn_stream(const uint16_t* x, const int32_t* expert_ids, const
     // fp32 partial sums reduced into hidden)
     // experts with more than ~32 rows on average take the wide kernels (up to 128 rows per pass)
     const bool wide = stream_wide(T, H, E, K, I);
-    const StreamShape gu = wide ? gateup_wide_shape(H) : gateup_shape(H);
+    const StreamShape gu = wide ? gateup_wide_shape(H) : gateup_shape(H, gateup_split);
     p.act = x;
     p.out = ws.hidden;
     p.partial = ws.partial;
@@ -1024,7 +1027,7 @@ hipError_t launch_ffn_stream(const uint16_t* x, const int32_t* expert_ids, const
     hipError_t err;
     {
         TraceScope trace("moe_ffn_gateup_swiglu", stream);
-        const int units = stream_gateup_grid(E, H, I, wide);
+        const int units = stream_gateup_grid(E, H, I, wide, gateup_split);
         if (wide) {
             p.kchunk = wide_chunk(gu.kc);
             err = launch_stream_wide<kSwiGLU>(p, units, stream);

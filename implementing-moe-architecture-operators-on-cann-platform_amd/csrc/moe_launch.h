@@ -55,10 +55,17 @@ struct FfnWorkspace {
     int32_t* slot_row;     // [T*K]   sorted row of each slot with a valid id (weight-streaming schedule only)
     int32_t* pscratch;     // the permute's per-slot ranks and per-chunk counts (tiled schedule only)
 };
-// tiled_split = false leaves out the tiled schedule's partial tiles (its down projection then runs unsplit)
-size_t ffn_workspace_bytes(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I, bool tiled_split = true);
+// The split-K variants a call may use, both on by default: tiled = the tiled schedule's split leftover round of
+// its down projection (up to 64 MiB of fp32 partial tiles), gateup = the 32-row streaming gate/up kernel's split
+// of an H too long for LDS (splits x T*K x 2I fp32 partial sums). Off, the down projection runs unsplit and a
+// long H runs 16-row streaming passes or the tiled schedule, with a smaller workspace.
+struct FfnSplits {
+    bool tiled = true;
+    bool gateup = true;
+};
+size_t ffn_workspace_bytes(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I, FfnSplits splits = {});
 FfnWorkspace ffn_workspace_carve(void* base, int64_t T, int64_t H, int64_t E, int64_t K, int64_t I,
-                                 bool tiled_split = true);
+                                 FfnSplits splits = {});
 
 int permute_block_threads();
 int permute_chunks(int S);
@@ -84,20 +91,22 @@ FfnGrid ffn_grid(int T, int H, int E, int K, int I);
 // weight-streaming schedule (moe_ffn_stream.hip)
 int stream_block_threads();
 int stream_rows_per_pass();
-bool stream_supported(int H, int I);
+bool stream_supported(int H, int I, bool gateup_split = true);
 // the wide weight-streaming kernels (up to 128 rows per pass): whether the shape allows them, and whether a call
 // of this size runs them
 bool stream_wide_supported(int H, int I);
 bool stream_wide(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I);
-hipError_t prepare_ffn_stream(int H, int I);  // kernel attributes, before the first launch of a call
-size_t stream_partial_bytes(int T, int H, int K, int I, bool wide);
-int stream_gateup_grid(int E, int H, int I, bool wide);
+// kernel attributes, before the first launch of a call
+hipError_t prepare_ffn_stream(int H, int I, bool gateup_split = true);
+size_t stream_partial_bytes(int T, int H, int K, int I, bool wide, bool gateup_split);
+int stream_gateup_grid(int E, int H, int I, bool wide, bool gateup_split = true);
 int stream_down_grid(int E, int H, int I);
 // with y non-null (and weights) the combine is produced too: by the split reduce when the down projection is
 // split over K, else by the combine kernel after the FFN
 hipError_t launch_ffn_stream(const uint16_t* x, const int32_t* expert_ids, const uint16_t* expert_weights,
                              uint16_t* expert_out, const FfnWorkspace& ws, int T, int H, int E, int K, int I,
-                             hipStream_t stream, const uint16_t* weights = nullptr, uint16_t* y = nullptr);
+                             hipStream_t stream, const uint16_t* weights = nullptr, uint16_t* y = nullptr,
+                             bool gateup_split = true);
 // LDS-tiled schedule (moe_ffn_tiled.hip)
 bool tiled_shape_supported(int64_t H, int64_t E, int64_t I);           // H, I granularity and LDS
 bool tiled_size_supported(int64_t T, int64_t H, int64_t K, int64_t I);  // 32-bit buffer offsets
@@ -116,12 +125,12 @@ hipError_t launch_ffn_tiled(const uint16_t* x, const uint16_t* expert_weights, u
 // schedule choice: 0 = weight streaming, 1 = LDS-tiled, -1 = no kernel supports the shape. A shape with many rows
 // per expert that the tiled kernels support except for their 32-bit offsets is -1, not the streaming schedule
 // (which would re-stream every expert's weights once per 32 rows).
-int ffn_schedule(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I);
+int ffn_schedule(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I, FfnSplits splits = {});
 // the whole FFN: permute (tiled schedule; the streaming schedule finds rows itself) and the two GEMMs. Every
 // kernel's attributes are set before the first launch, so a failure there leaves nothing launched.
 hipError_t launch_ffn(const uint16_t* x, const int32_t* expert_ids, const uint16_t* expert_weights,
                       uint16_t* expert_out, FfnWorkspace ws, int T, int H, int E, int K, int I, hipStream_t stream,
-                      bool tiled_split = true);
+                      FfnSplits splits = {});
 // the FFN followed by the combine: expert_out as launch_ffn writes it, y as launch_combine would compute it
 hipError_t launch_ffn_combine(const uint16_t* x, const int32_t* expert_ids, const uint16_t* weights,
                               const uint16_t* expert_weights, uint16_t* expert_out, uint16_t* y, FfnWorkspace ws,

@@ -271,8 +271,20 @@ moe_status moe_expert_ffn_no_alloc(const uint16_t* x, const int32_t* expert_ids,
         return fail(MOE_ERR_NULL, "MoeExpertFFN (no alloc): null tensor pointer");
     if (!aligned16(x) || !aligned16(expert_weights) || !aligned16(expert_out))
         return fail(MOE_ERR_UNSUPPORTED, "MoeExpertFFN (no alloc): x, expert_weights, expert_out must be 16-byte aligned");
-    // the tiled schedule runs its down projection unsplit here: its split partial tiles alone take up to 64 MiB
-    const size_t need = moe::ffn_workspace_bytes(T, H, E, K, I, /*tiled_split=*/false);
+    // the tiled schedule runs its down projection unsplit here (its split partial tiles alone take up to 64 MiB);
+    // the streaming gate/up kernel splits a long H only if its partial sums fit, else the call runs that H unsplit
+    moe::FfnSplits splits;
+    splits.tiled = false;
+    size_t need = moe::ffn_workspace_bytes(T, H, E, K, I, splits);
+    if (need > moe::noalloc_scratch_bytes()) {
+        moe::FfnSplits compact = splits;
+        compact.gateup = false;
+        if (moe::ffn_schedule(T, H, E, K, I, compact) >= 0 &&
+            moe::ffn_workspace_bytes(T, H, E, K, I, compact) <= moe::noalloc_scratch_bytes()) {
+            splits = compact;
+            need = moe::ffn_workspace_bytes(T, H, E, K, I, splits);
+        }
+    }
     if (need > moe::noalloc_scratch_bytes())
         return fail(MOE_ERR_UNSUPPORTED,
                     "MoeExpertFFN (no alloc): T=%lld H=%lld E=%lld K=%lld I=%lld needs %zu bytes of workspace, the "
@@ -282,10 +294,9 @@ moe_status moe_expert_ffn_no_alloc(const uint16_t* x, const int32_t* expert_ids,
     void* scratch = nullptr;
     hipError_t err = moe::noalloc_scratch(&scratch);
     if (err != hipSuccess) return hip_fail(err, "MoeExpertFFN (no alloc): scratch address");
-    const moe::FfnWorkspace ws = moe::ffn_workspace_carve(scratch, T, H, E, K, I, /*tiled_split=*/false);
+    const moe::FfnWorkspace ws = moe::ffn_workspace_carve(scratch, T, H, E, K, I, splits);
     err = moe::launch_ffn(x, expert_ids, expert_weights, expert_out, ws, static_cast<int>(T), static_cast<int>(H),
-                          static_cast<int>(E), static_cast<int>(K), static_cast<int>(I), as_stream(stream),
-                          /*tiled_split=*/false);
+                          static_cast<int>(E), static_cast<int>(K), static_cast<int>(I), as_stream(stream), splits);
     if (err != hipSuccess) return hip_fail(err, "MoeExpertFFN (no alloc) GEMM launch");
     return ok();
 }

@@ -186,9 +186,11 @@ moe_status moe_combine(const uint16_t* expert_out, const int32_t* expert_ids, co
  * forbid hipMalloc.
  * The workspace is a fixed per-GPU device array inside the library (64 MiB, held by every GPU the library runs
  * on until the process ends). Sizes whose workspace exceeds it return MOE_ERR_UNSUPPORTED before anything is
- * launched (e.g. T*K*I*2 > ~60 MiB; the LDS-tiled schedule
- * runs its down projection without the split leftover round here, so expert_out can differ from
- * moe_expert_ffn's in fp32 summation order on that schedule; the weight-streaming schedule is bit-identical).
+ * launched (e.g. T*K*I*2 > ~60 MiB). The LDS-tiled schedule runs its down projection without the split
+ * leftover round here, so expert_out can differ from moe_expert_ffn's in fp32 summation order on that schedule.
+ * The weight-streaming schedule is bit-identical, except that an H above 2272 whose split gate/up partial sums
+ * (splits x T*K x 2I x 4 bytes) do not fit runs gate/up unsplit (16-row passes, or the tiled schedule when H
+ * exceeds 4568), with the same difference in summation order.
  * Every call on a GPU shares that GPU's array: calls that overlap on one GPU (two streams or threads) race.
  * The first call on each device looks up that device's array address and sets the kernels' LDS limits: make it
  * outside graph capture (one eager call per device); later calls may be captured and replayed.
