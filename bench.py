@@ -28,7 +28,9 @@ Then two library kernels over 1 GiB give this box's achievable HBM rates next to
 roofline uses: a whole-line non-temporal streaming read (`hbm_read_gbps`, the access the decode weight stream
 uses) and a plain copy (`hbm_copy_gbps`, read + write); and the vendor library's dense fp16 GEMM (hipBLASLt
 through torch.matmul, 8192 x 8192 x 8192, A @ B^T) gives its achievable MFMA rate next to the published
-2.5 PFLOP/s (`gemm_fp16_tflops_library`). On the decode workload a prefill pass follows (BASELINE.json
+2.5 PFLOP/s (`gemm_fp16_tflops_library`); on workloads of at least 64 rows per expert (and on the prefill pass)
+its batched GEMM on the expert GEMMs' own shapes, T*K/E rows for every expert, gives the library's time for the
+same flops without the gather, SwiGLU, scatter or ragged experts (`library_bmm`). On the decode workload a prefill pass follows (BASELINE.json
 configs[2], T=8192 with the same weights): its FFN time and MFMA fraction are `prefill_ffn_us`,
 `prefill_ffn_tflops` and `prefill_ffn_mfma_frac` (the north_star's second target), its kernels under `prefill`.
 Kernels whose per-launch inputs fit the 256 MB Infinity
@@ -111,6 +113,32 @@ def cpu_model() -> str:
     except OSError:
         pass
     return platform.processor() or "unknown"
+
+
+def library_bmm_us(torch, dev, T: int, H: int, E: int, K: int, I: int) -> dict:
+    """The vendor library's batched fp16 GEMM (hipBLASLt through torch.bmm, fp32 accumulation) on the expert GEMMs'
+    shapes with T*K/E rows for every expert: gate/up [E, m, H] x [E, H, 2I], down [E, m, I] x [E, I, H]. A dense
+    stand-in for the grouped GEMMs without the row gather, SwiGLU, scatter or ragged experts; both operands
+    contiguous. Average event time of 20 launches after 10 warm-up launches (the clock ramps over the first)."""
+    m = T * K // E
+    out = {"rows_per_expert": m}
+    for name, kdim, ndim in (("gateup", H, 2 * I), ("down", I, H)):
+        a = torch.randn(E, m, kdim, device=dev, dtype=torch.float16)
+        b = torch.randn(E, kdim, ndim, device=dev, dtype=torch.float16).contiguous()
+        c = torch.empty(E, m, ndim, device=dev, dtype=torch.float16)
+        for _ in range(10):
+            torch.bmm(a, b, out=c)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(20):
+            torch.bmm(a, b, out=c)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / 20 * 1e3
+        out[f"{name}_us"] = round(us, 2)
+        out[f"{name}_mfma_frac"] = round(2 * E * m * kdim * ndim / (us * 1e-6) / 1e12 / MFMA_FP16_PEAK_TFLOPS, 4)
+        del a, b, c
+    return out
 
 
 def calibrate_copy(ops, torch, args) -> int:
@@ -390,6 +418,10 @@ def main() -> int:
         progress(f"prefill T={PT}: layer {prefill['layer_us']} us, FFN {prefill['ffn_us']} us = "
                  f"{prefill['ffn_tflops']} TFLOP/s ({prefill['ffn_mfma_frac'] * 100:.1f}% of fp16 peak)")
         del px, pwg, pids, pw, peo, py, pws
+        if not args.no_copy_rate:
+            lib_bmm = library_bmm_us(torch, dev, PT, H, E, K, I)
+            prefill["library_bmm"] = lib_bmm
+            progress(f"prefill shapes through the library's batched GEMM: {lib_bmm}")
 
     ids_h = ids.cpu().numpy()
     active = int((np.bincount(ids_h.ravel(), minlength=E) > 0).sum())
@@ -480,6 +512,7 @@ def main() -> int:
         "hbm_copy_gbps": copy_gbps,
         "hbm_read_gbps": read_gbps,
         "gemm_fp16_tflops_library": gemm_tflops,
+        "library_bmm": library_bmm_us(torch, dev, T, H, E, K, I) if not args.no_copy_rate and T * K >= 64 * E else None,
         "prefill_ffn_us": prefill["ffn_us"] if prefill else None,
         "prefill_ffn_tflops": prefill["ffn_tflops"] if prefill else None,
         "prefill_ffn_mfma_frac": prefill["ffn_mfma_frac"] if prefill else None,
