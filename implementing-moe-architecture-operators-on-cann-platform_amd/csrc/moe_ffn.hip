@@ -73,8 +73,9 @@ size_t ffn_workspace_bytes(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I
     bytes += align_up(sizeof(uint16_t) * S * static_cast<size_t>(I), 256);
     const int schedule = ffn_schedule(T, H, E, K, I, splits);
     if (schedule == 0) {
-        bytes += align_up(stream_partial_bytes(static_cast<int>(T), static_cast<int>(H), static_cast<int>(K),
-                                               static_cast<int>(I), stream_wide(T, H, E, K, I), splits.gateup), 256);
+        bytes += align_up(stream_partial_bytes(static_cast<int>(T), static_cast<int>(H), static_cast<int>(E),
+                                               static_cast<int>(K), static_cast<int>(I), stream_wide(T, H, E, K, I),
+                                               splits.gateup), 256);
         bytes += align_up(sizeof(int32_t) * S, 256);
     } else if (schedule == 1) {
         bytes += align_up(permute_scratch_bytes(static_cast<int>(S), static_cast<int>(E)), 256);
@@ -102,8 +103,9 @@ FfnWorkspace ffn_workspace_carve(void* base, int64_t T, int64_t H, int64_t E, in
     const int schedule = ffn_schedule(T, H, E, K, I, splits);
     if (schedule == 0) {
         ws.partial = reinterpret_cast<float*>(p);
-        p += align_up(stream_partial_bytes(static_cast<int>(T), static_cast<int>(H), static_cast<int>(K),
-                                           static_cast<int>(I), stream_wide(T, H, E, K, I), splits.gateup), 256);
+        p += align_up(stream_partial_bytes(static_cast<int>(T), static_cast<int>(H), static_cast<int>(E),
+                                           static_cast<int>(K), static_cast<int>(I), stream_wide(T, H, E, K, I),
+                                           splits.gateup), 256);
         ws.slot_row = reinterpret_cast<int32_t*>(p);
     } else if (schedule == 1) {
         ws.pscratch = reinterpret_cast<int32_t*>(p);
@@ -125,7 +127,7 @@ FfnGrid ffn_grid(int T, int H, int E, int K, int I) {
         g.rows_per_tile = tiled_rows_per_tile();
     } else {
         g.block_threads = stream_block_threads();
-        g.gateup_blocks = stream_gateup_grid(E, H, I, stream_wide(T, H, E, K, I));
+        g.gateup_blocks = stream_gateup_grid(T, H, E, K, I, stream_wide(T, H, E, K, I));
         g.down_blocks = stream_down_grid(E, H, I);
         g.rows_per_tile = stream_rows_per_pass();
     }
@@ -144,7 +146,7 @@ hipError_t launch_ffn(const uint16_t* x, const int32_t* expert_ids, const uint16
             return launch_ffn_tiled(x, expert_weights, expert_out, ws, T, H, E, K, I, stream, splits.tiled);
         }
         case 0: {
-            const hipError_t err = prepare_ffn_stream(H, I, splits.gateup);
+            const hipError_t err = prepare_ffn_stream(H, I);
             if (err != hipSuccess) return err;
             return launch_ffn_stream(x, expert_ids, expert_weights, expert_out, ws, T, H, E, K, I, stream, nullptr,
                                      nullptr, splits.gateup);

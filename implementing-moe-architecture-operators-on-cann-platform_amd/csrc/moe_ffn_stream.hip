@@ -834,23 +834,29 @@ StreamShape pick_shape(int kdim, bool allow_split) {
 }
 
 // Gate/up needs the whole of H per unit for its SwiGLU. When 32 rows of the whole H do not fit the LDS (H above
-// ~2200), each unit covers one K-range of H at 32 rows instead and writes fp32 gate and up sums (kGatePartial),
+// 2272), each unit covers one K-range of H at 32 rows instead and writes fp32 gate and up sums (kGatePartial),
 // which gateup_reduce_kernel adds before the SwiGLU: one more launch and 2 * nsplit * 4 bytes per (row, i) of
-// traffic, where the whole-H layout holds 16 rows (an expert with more rows re-streams its weights per 16 rows)
-// or none at all.
+// traffic, where the whole-H layout holds 16 rows (an expert with more rows re-streams its weights per 16 rows;
+// up to H = 4568) or none at all. K-ranges are multiples of 256 (the deepest ring): at H = 2336 the only split
+// is 73 K-ranges of 32, and the FFN took 473.5 us against 183.3 us unsplit (T = 64, E = 16, K = 2, I = 4096).
 StreamShape gateup_split_shape(int H) {
     const int kc_max = (kLdsMax - kTbBytes) / (kMaxRows * 2) - 8;
-    for (int d = 8; d >= 1; d /= 2) {
-        int best = 0;
-        for (int kc = 32 * d; kc <= kc_max && kc <= H; kc += 32 * d)
-            if (H % kc == 0) best = kc;
-        if (best > 0) return StreamShape{best, d, kMaxRows, H / best};
-    }
-    return StreamShape{0, 0, 0, 0};
+    int best = 0;
+    for (int kc = 256; kc <= kc_max && kc <= H; kc += 256)
+        if (H % kc == 0) best = kc;
+    return best > 0 ? StreamShape{best, 8, kMaxRows, H / best} : StreamShape{0, 0, 0, 0};
 }
-StreamShape gateup_shape(int H, bool allow_split) {
+// Average rows per expert from which the 32-row kernel splits an H that 16 rows fit whole: below it one 16-row
+// pass covers most experts and the partial sums are extra traffic. The FFN at E = 16, K = 2, I = 4096, 16-row
+// passes over the whole H / split (us):
+//   H = 2816 (11 K-ranges): 8 rows per expert 186.7 / 229.8, 24 rows 311.6 / 272.2
+//   H = 3072 (2 K-ranges):  8 rows 202.0 / 212.1, 24 rows 339.7 / 236.1
+//   H = 4096 (2 K-ranges):  8 rows 254.0 / 274.7, 24 rows 533.8 / 435.5; Mixtral's E = 8, I = 14336 at 16 rows
+//                           643 / 514
+constexpr int64_t kGateUpSplitMinRows = 12;
+StreamShape gateup_shape(int64_t T, int H, int64_t E, int64_t K, bool allow_split) {
     const StreamShape whole = pick_shape(H, false);
-    if (whole.kc > 0 && whole.rows_cap == kMaxRows) return whole;
+    if (whole.kc > 0 && (whole.rows_cap == kMaxRows || T * K < kGateUpSplitMinRows * E)) return whole;
     const StreamShape split = allow_split ? gateup_split_shape(H) : StreamShape{0, 0, 0, 0};
     return split.kc > 0 ? split : whole;
 }
@@ -930,12 +936,18 @@ const void* stream_kernel_fn(int d) {
 
 }  // namespace
 
-hipError_t prepare_ffn_stream(int H, int I, bool gateup_split) {
-    const StreamShape gu = gateup_shape(H, gateup_split), dn = pick_shape(I, true);
-    const void* fns[2] = {gu.nsplit > 1 ? stream_kernel_fn<kGatePartial>(gu.d) : stream_kernel_fn<kSwiGLU>(gu.d),
+hipError_t prepare_ffn_stream(int H, int I) {
+    // the 32-row gate/up kernel of either layout that the call's size may pick: whole H, or H split into K-ranges
+    const StreamShape whole = pick_shape(H, false), split = gateup_split_shape(H), dn = pick_shape(I, true);
+    const void* gu_fns[2] = {whole.kc > 0 ? stream_kernel_fn<kSwiGLU>(whole.d) : nullptr,
+                             split.kc > 0 && whole.rows_cap != kMaxRows ? stream_kernel_fn<kGatePartial>(split.d)
+                                                                        : nullptr};
+    if (!gu_fns[0] && !gu_fns[1]) return hipErrorInvalidValue;
+    const void* fns[3] = {gu_fns[0], gu_fns[1],
                           dn.nsplit > 1 ? stream_kernel_fn<kPartial>(dn.d) : stream_kernel_fn<kScatter>(dn.d)};
+    if (!fns[2]) return hipErrorInvalidValue;
     for (const void* fn : fns) {
-        if (!fn) return hipErrorInvalidValue;
+        if (!fn) continue;
         const hipError_t err = ensure_lds_limit(fn, kLdsMax);
         if (err != hipSuccess) return err;
     }
@@ -957,8 +969,9 @@ int stream_rows_per_pass() { return kMaxRows; }
 
 // One fp32 buffer serves both splits in turn: gate/up's sums are reduced into hidden before the down projection
 // writes its own. The wide gate/up kernel never splits H.
-size_t stream_partial_bytes(int T, int H, int K, int I, bool wide, bool gateup_split) {
-    const StreamShape gu = wide ? gateup_wide_shape(H) : gateup_shape(H, gateup_split), dn = pick_shape(I, true);
+size_t stream_partial_bytes(int T, int H, int E, int K, int I, bool wide, bool gateup_split) {
+    const StreamShape gu = wide ? gateup_wide_shape(H) : gateup_shape(T, H, E, K, gateup_split);
+    const StreamShape dn = pick_shape(I, true);
     const size_t rows = static_cast<size_t>(T) * K;
     const size_t g = gu.nsplit > 1 ? static_cast<size_t>(gu.nsplit) * rows * 2 * I * sizeof(float) : 0;
     const size_t d = dn.nsplit > 1 ? static_cast<size_t>(dn.nsplit) * rows * H * sizeof(float) : 0;
@@ -966,7 +979,8 @@ size_t stream_partial_bytes(int T, int H, int K, int I, bool wide, bool gateup_s
 }
 
 bool stream_supported(int H, int I, bool gateup_split) {
-    return gateup_shape(H, gateup_split).kc > 0 && pick_shape(I, true).kc > 0;
+    const bool gu = pick_shape(H, false).kc > 0 || (gateup_split && gateup_split_shape(H).kc > 0);
+    return gu && pick_shape(I, true).kc > 0;
 }
 
 // Whether the shape can run the wide kernels (both GEMMs' rings and K-ranges allow a chunked stage).
@@ -980,9 +994,9 @@ bool stream_wide(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
     return T * K >= kWideMinRows * E && stream_wide_supported(static_cast<int>(H), static_cast<int>(I));
 }
 
-int stream_gateup_grid(int E, int H, int I, bool wide, bool gateup_split) {
+int stream_gateup_grid(int T, int H, int E, int K, int I, bool wide, bool gateup_split) {
     return E * ((I + kWaves * 16 - 1) / (kWaves * 16)) *
-           (wide ? gateup_wide_shape(H) : gateup_shape(H, gateup_split)).nsplit;
+           (wide ? gateup_wide_shape(H) : gateup_shape(T, H, E, K, gateup_split)).nsplit;
 }
 
 int stream_down_grid(int E, int H, int I) {
@@ -1011,7 +1025,7 @@ hipError_t launch_ffn_stream(const uint16_t* x, const int32_t* expert_ids, const
     // fp32 partial sums reduced into hidden)
     // experts with more than ~32 rows on average take the wide kernels (up to 128 rows per pass)
     const bool wide = stream_wide(T, H, E, K, I);
-    const StreamShape gu = wide ? gateup_wide_shape(H) : gateup_shape(H, gateup_split);
+    const StreamShape gu = wide ? gateup_wide_shape(H) : gateup_shape(T, H, E, K, gateup_split);
     p.act = x;
     p.out = ws.hidden;
     p.partial = ws.partial;
@@ -1027,7 +1041,7 @@ hipError_t launch_ffn_stream(const uint16_t* x, const int32_t* expert_ids, const
     hipError_t err;
     {
         TraceScope trace("moe_ffn_gateup_swiglu", stream);
-        const int units = stream_gateup_grid(E, H, I, wide, gateup_split);
+        const int units = stream_gateup_grid(T, H, E, K, I, wide, gateup_split);
         if (wide) {
             p.kchunk = wide_chunk(gu.kc);
             err = launch_stream_wide<kSwiGLU>(p, units, stream);

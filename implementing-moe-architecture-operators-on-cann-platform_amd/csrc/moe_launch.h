@@ -96,10 +96,9 @@ bool stream_supported(int H, int I, bool gateup_split = true);
 // of this size runs them
 bool stream_wide_supported(int H, int I);
 bool stream_wide(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I);
-// kernel attributes, before the first launch of a call
-hipError_t prepare_ffn_stream(int H, int I, bool gateup_split = true);
-size_t stream_partial_bytes(int T, int H, int K, int I, bool wide, bool gateup_split);
-int stream_gateup_grid(int E, int H, int I, bool wide, bool gateup_split = true);
+hipError_t prepare_ffn_stream(int H, int I);  // kernel attributes, before the first launch of a call
+size_t stream_partial_bytes(int T, int H, int E, int K, int I, bool wide, bool gateup_split);
+int stream_gateup_grid(int T, int H, int E, int K, int I, bool wide, bool gateup_split = true);
 int stream_down_grid(int E, int H, int I);
 // with y non-null (and weights) the combine is produced too: by the split reduce when the down projection is
 // split over K, else by the combine kernel after the FFN

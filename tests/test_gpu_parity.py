@@ -481,7 +481,8 @@ def test_ffn_wide_streaming_schedule(ops, T, H, E, K, I, pattern):
 
 
 @pytest.mark.parametrize("T,H,E,K,I,pattern,nsplit", [
-    (24, 4096, 8, 2, 256, "uniform", 2),   # 32-row kernel, H in two K-ranges of 2048
+    (64, 4096, 8, 2, 256, "uniform", 2),   # 32-row kernel, H in two K-ranges of 2048 (16 rows per expert)
+    (24, 4096, 8, 2, 256, "uniform", 1),   # 6 rows per expert: one 16-row pass over the whole H, no partial sums
     (40, 7168, 16, 4, 128, "invalid", 4),  # DeepSeek-V3's H in four K-ranges of 1792, ids outside [0, E)
     (100, 2816, 8, 2, 96, "skewed", 11),   # eleven K-ranges of 256; one expert 150 rows (5 passes), I tail
     (512, 7168, 16, 2, 128, "zipf", 1),    # wide kernel (64 rows per expert): all of H in 14 stages of 512
@@ -490,7 +491,8 @@ def test_ffn_wide_streaming_schedule(ops, T, H, E, K, I, pattern):
 def test_ffn_streaming_large_hidden(ops, T, H, E, K, I, pattern, nsplit):
     """H too large for 32 rows of x to sit in LDS whole: the 32-row gate/up kernel splits H into nsplit
     K-ranges, each workgroup writes its range's fp32 gate and up partial sums, and a reduce kernel adds the ranges
-    in order and applies SwiGLU; the wide kernel (from 32 rows per expert) stages all of H in chunks instead. The
+    in order and applies SwiGLU; below 12 rows per expert an H that 16 rows fit (up to 4568) runs 16-row passes
+    over the whole of it instead, and the wide kernel (from 32 rows per expert) stages all of H in chunks. The
     plan's gate/up grid shows the split (E x ceil(I / 128) column blocks x nsplit); offsets / sorted_slot and
     expert_out against the oracle on every slot."""
     import ctypes as C
