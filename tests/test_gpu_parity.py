@@ -792,6 +792,31 @@ def test_deepseek_v3_layer_shape_sampled(ops):
         assert torch.equal(a, b), name
 
 
+@pytest.mark.parametrize("T,H,E,K,I", [
+    (64, 4096, 8, 2, 512),   # gate/up in two K-ranges of 2048, then the down projection and the combine
+    (24, 7168, 16, 4, 256),  # DeepSeek-V3's H: four K-ranges of 1792
+])
+def test_layer_with_gateup_split(ops, T, H, E, K, I):
+    """moe_layer at a long H on the streaming schedule (the gate/up kernel splits H, a reduce adds the K-ranges):
+    routing against the oracle on every token, expert_out against the oracle FFN on every slot, y bit for bit
+    the oracle combine of expert_out, and every output equal to the three operators' run bit for bit."""
+    cfg = synth.MoeConfig(T, H, E, K, I, name="gateup_split_layer")
+    log(f"[layer split] T={T} H={H} E={E} K={K} I={I}")
+    x_d, wg_d, ew_d = gpu_inputs(ops, cfg, 46)
+    y_d, ids_d, w_d, eo_d = ops.moe_layer_fused(x_d, wg_d, ew_d, K)
+    ref = ops.moe_layer(x_d, wg_d, ew_d, K)
+    for name, a, b in zip(("y", "ids", "weights", "expert_out"), ref, (y_d, ids_d, w_d, eo_d)):
+        assert torch.equal(a, b), name
+    x, ids, w = host(x_d), host(ids_d), host(w_d)
+    check_routing(ids, w, x, host(wg_d), K, "layer split")
+    eo_o = oracle_ffn_threads(f32(x), ids, f32(host(ew_d)), I)
+    m = oracle.compare(f32(host(eo_d)), eo_o)
+    log(f"[layer split] expert_out vs oracle on all {T} tokens: {m}")
+    within(m, max_abs=1e-2, mean_abs=1e-3, cos=0.9999)
+    y_o = oracle.combine(f32(host(eo_d)), f32(w)).astype(np.float16)
+    assert np.array_equal(host(y_d).view(np.uint16), y_o.view(np.uint16))
+
+
 def test_reference_target_case_seed44(ops):
     """The reference's own target-size RunTest case (tests/moe_cpu_sim.cpp:862-864: T=128, H=2048, E=16, K=2,
     I=8192, seed 44) on its own generator's inputs rounded to fp16: ids bit-exact against the reference's
