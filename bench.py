@@ -171,6 +171,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="decode", help="workload (synth.CONFIGS); the driver uses the default")
+    ap.add_argument("--shape", default=None, metavar="T,H,E,K,I",
+                    help="another workload of this shape instead of --config (named 'custom')")
+    ap.add_argument("--zipf", action="store_true", help="with --shape: Zipf-skewed routing, as the deepseek config")
     ap.add_argument("--seed", type=int, default=44)
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the reference CPU timing")
     ap.add_argument("--cpu-target-gflop", type=float, default=30.0,
@@ -198,7 +201,10 @@ def main() -> int:
     lib = importlib.import_module(PKG).load_library()
     if args.calibrate_copy:
         return calibrate_copy(ops, torch, args)
-    cfg = synth.CONFIGS[args.config]
+    if args.shape:
+        cfg = synth.MoeConfig(*(int(v) for v in args.shape.split(",")), zipf=args.zipf, name="custom")
+    else:
+        cfg = synth.CONFIGS[args.config]
     T, H, E, K, I = cfg.T, cfg.H, cfg.E, cfg.K, cfg.I
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)

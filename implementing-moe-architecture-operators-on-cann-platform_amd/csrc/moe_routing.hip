@@ -624,6 +624,11 @@ __global__ __launch_bounds__(kWideWaves * kWave) void routing_wide_kernel(const 
 // 0, a 16-byte aligned w_gate, SK dividing H / 32), for every T, so a token's bits do not depend on its batch.
 // At E <= 64 it was slower than the narrow kernel (T = 16384, E = 64: 27.8 µs alone and 34.2 µs in the layer,
 // against 21.8 and 30.2 µs): every wave reads all of w_gate from LDS, four times the narrow kernel's share.
+// At few tokens each 16-token block multiplies all of w_gate on one CU, so the time does not fall with T: H = 7168,
+// E = 256 (3.7 MB of w_gate) 140 µs at T = 1, 185 µs at T = 128 to 2048. Measured and not kept (bit-identical
+// ids and weights): workgroups of 1 or 2 waves (16 or 32 tokens, more CUs) 137 / 145 µs at T = 128 but 385 / 362 µs
+// at T = 16384; a 7-stage w_gate ring (96 KB in flight) 187 µs. Splitting H over waves or CUs would make a
+// token's summation order depend on T, or need a workspace, which MoeRoutingTopK does not take.
 // The selection then runs on the accumulators: the MFMA leaves lane (row kg = lane / 16, column n) with token
 // 4 kg + r, expert 16 b + n in acc[b][r], i.e. each 16-lane DPP row holds one token's experts as select_vals
 // wants them.
