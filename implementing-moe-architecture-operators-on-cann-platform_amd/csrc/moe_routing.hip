@@ -20,11 +20,12 @@
 //            renormalisation with all-reduces over the token's lanes (select_row): max,
 //            expf(l - max), sum, division by the sum; K rounds of an arg-max (lowest index wins an exact tie); the
 //            renormalising sum over the K picks in rank order; fp16 round-to-nearest-even.
-// For E > 64 the rows kernel runs: a workgroup owns 64 tokens and each of its 4 waves 16 of them over all of H,
-// so no partials are folded and the selection runs on the accumulators. w_gate stages (16 KB, row-major) are
-// copied into LDS with 16-byte direct-to-LDS loads and shared by the 4 waves; each wave's x rows stream through its
-// own LDS ring 16 k-steps ahead. T = 16384, H = 2048: E = 256, K = 8 75.7 us; E = 128 42.5 us (the wide kernel
-// below: 171.7 and 95.1 us). When w_gate cannot be copied 16 bytes at a time (E % 8 != 0, unaligned) the wide
+// For E > 64 the rows kernel runs above 8192 tokens: a workgroup owns 64 tokens and each of its 4 waves 16 of them
+// over all of H, so the selection runs on the accumulators. w_gate stages (16 KB, row-major) are copied into LDS
+// with 16-byte direct-to-LDS loads and shared by the 4 waves; each wave's x rows stream through its own LDS ring
+// 16 k-steps ahead. Up to 8192 tokens the quarters kernel runs: a workgroup owns 16 tokens and each of its 4 waves
+// one quarter of H. Both add a token's H in the same four quarter sums, so the two give the same bits.
+// T = 16384, H = 2048: E = 256, K = 8 75.8 us; E = 128 39.0 us (the wide kernel below: 171.7 and 95.1 us). When w_gate cannot be copied 16 bytes at a time (E % 8 != 0, unaligned) the wide
 // kernel runs instead: its w_gate chunks are read with coalesced loads and written transposed, [expert][h], so a
 // lane's B fragment is one ds_read_b128; a stage of 2-4 chunks is loaded into registers while the previous one is
 // multiplied, two LDS buffers, one barrier per stage.
@@ -620,18 +621,28 @@ __global__ __launch_bounds__(kWideWaves * kWave) void routing_wide_kernel(const 
 //   * each wave copies its 16 token rows of x (64 B per row and k-step) into its own LDS ring, kRowXDepth k-steps
 //     ahead of their use, so each CU keeps ~64 KB of x in flight without spending registers on it;
 //   * A fragments are ds_read_b128 from the x ring, B fragments two ds_read_b64_tr_b16 from the w_gate stage.
-// The k-steps add in order into one accumulator set. The kernel runs for E > 64 whenever its copies can (E % 8 ==
-// 0, a 16-byte aligned w_gate, SK dividing H / 32), for every T, so a token's bits do not depend on its batch.
+// The k-steps of each quarter of H add in order (quarter_begin below). The kernel runs for E > 64 whenever its
+// copies can (E % 8 == 0, a 16-byte aligned w_gate, SK dividing H / 32) and T > 8192; the quarters kernel gives
+// the same bits below that, so a token's bits do not depend on its batch.
 // At E <= 64 it was slower than the narrow kernel (T = 16384, E = 64: 27.8 µs alone and 34.2 µs in the layer,
 // against 21.8 and 30.2 µs): every wave reads all of w_gate from LDS, four times the narrow kernel's share.
-// At few tokens each 16-token block multiplies all of w_gate on one CU, so the time does not fall with T: H = 7168,
-// E = 256 (3.7 MB of w_gate) 140 µs at T = 1, 185 µs at T = 128 to 2048. Measured and not kept (bit-identical
-// ids and weights): workgroups of 1 or 2 waves (16 or 32 tokens, more CUs) 137 / 145 µs at T = 128 but 385 / 362 µs
-// at T = 16384; a 7-stage w_gate ring (96 KB in flight) 187 µs. Splitting H over waves or CUs would make a
-// token's summation order depend on T, or need a workspace, which MoeRoutingTopK does not take.
+// At few tokens each 16-token block multiplies all of w_gate on one CU, and the compiler's wait for every copy in
+// flight before a transposing read (see the quarters kernel) leaves the ring no deeper than one stage, so the time
+// does not fall with T: H = 7168, E = 256 (3.7 MB of w_gate) 140 µs at T = 1, 185 µs at T = 128 to 2048, where
+// the quarters kernel takes 44-55 µs. Measured before it and not kept: workgroups of 1 or 2 waves (16 or 32
+// tokens, more CUs) 137 / 145 µs at T = 128 but 385 / 362 µs at T = 16384; a 7-stage w_gate ring 187 µs; the
+// rows kernel double-buffered with each stage read whole before the next one's copies, as the quarters kernel
+// does, 192 µs at T = 128 and 2x slower at E = 128.
 // The selection then runs on the accumulators: the MFMA leaves lane (row kg = lane / 16, column n) with token
 // 4 kg + r, expert 16 b + n in acc[b][r], i.e. each 16-lane DPP row holds one token's experts as select_vals
 // wants them.
+// The H reduction of the rows and quarters kernels: the stages fall into four quarters (quarter j = stages
+// [j nst / 4, (j + 1) nst / 4)), each summed in k order from zero, and the quarter sums are added as
+// ((q0 + q1) + q2) + q3. The rows kernel sums the quarters one after the other in each wave; the quarters kernel
+// gives each quarter to a wave of its own. Both make the same fp32 operations for a token, so its logits, ids and
+// weights do not depend on which of them ran.
+__device__ __forceinline__ int quarter_begin(int j, int nst) { return j * nst / 4; }
+
 constexpr int kRowWaves = 4;
 constexpr int kRowTokens = 16 * kRowWaves;
 constexpr int kRowXDepth = 16;                                               // x k-steps in flight per wave
@@ -708,41 +719,56 @@ __global__ __launch_bounds__(kRowWaves * kWave) void routing_rows_kernel(const u
                                                      16, xoff, (st * SK + ks) * 64, 0, 0);
     };
 
-    f32x4 acc[EB];
+    f32x4 acc[EB];   // the current quarter's sum
+    f32x4 qsum[EB];  // the finished quarters' sum, ((q0 + q1) + q2)
 #pragma unroll
-    for (int b = 0; b < EB; ++b) acc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int b = 0; b < EB; ++b) acc[b] = qsum[b] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     // Issue order: x(0 .. NXS-1), w(0 .. NW-2), then per iteration j: w(j + NW - 1), x(j + NXS).
     for (int st = 0; st < min(NXS, nst); ++st) issue_x(st);
     for (int st = 0; st < min(NW - 1, nst); ++st) issue_w(st);
-    for (int i = 0; i < nst; ++i) {
-        // This wave's copies of w_gate stage i and of x stage i have landed. After w(i) (iteration i - NW + 1, or
-        // the prologue) came x(i - NW + 1 + NXS) and then NW - 2 iterations of w + x: SK + (NW - 2)(4 + SK) copies
-        // when every one of them went out, i.e. when iteration i - 1 still issued both; otherwise wait for all.
-        // x(i) went out no later than iteration i - NXS <= i - NW, before w(i).
-        if (i >= NW - 1 && i + NW - 2 < nst && i - 1 + NXS < nst) {
-            __builtin_amdgcn_s_waitcnt(vmcnt_imm(SK + (NW - 2) * (4 + SK)));
-        } else {
-            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-        }
-        __syncthreads();  // every wave's w(i) is visible; every wave is done with w(i - 1) and its x(i - 1)
-        if (i + NW - 1 < nst) issue_w(i + NW - 1);
-        if (i + NXS < nst) issue_x(i + NXS);
-        const uint8_t* ws = wbuf + (i % NW) * kStage;
-        const uint8_t* xs = xbuf + (i % XR) * SK * 1024;
+    // The quarters run one after the other (the copies run on across their boundaries); each starts from zero and
+    // joins the sum when it ends.
+    int i = 0;
+    for (int j = 0; j < 4; ++j) {
+        for (const int iend = quarter_begin(j + 1, nst); i < iend; ++i) {
+            // This wave's copies of w_gate stage i and of x stage i have landed. After w(i) (iteration i - NW + 1, or
+            // the prologue) came x(i - NW + 1 + NXS) and then NW - 2 iterations of w + x: SK + (NW - 2)(4 + SK) copies
+            // when every one of them went out, i.e. when iteration i - 1 still issued both; otherwise wait for all.
+            // x(i) went out no later than iteration i - NXS <= i - NW, before w(i).
+            if (i >= NW - 1 && i + NW - 2 < nst && i - 1 + NXS < nst) {
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm(SK + (NW - 2) * (4 + SK)));
+            } else {
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+            }
+            __syncthreads();  // every wave's w(i) is visible; every wave is done with w(i - 1) and its x(i - 1)
+            if (i + NW - 1 < nst) issue_w(i + NW - 1);
+            if (i + NXS < nst) issue_x(i + NXS);
+            const uint8_t* ws = wbuf + (i % NW) * kStage;
+            const uint8_t* xs = xbuf + (i % XR) * SK * 1024;
 #pragma unroll
-        for (int ks = 0; ks < SK; ++ks) {
-            const f16x8 a = *reinterpret_cast<const f16x8*>(xs + ks * 1024 + arow * 64 + kg * 16);
-            const uint8_t* wk = ws + ks * 32 * Epad * 2;
+            for (int ks = 0; ks < SK; ++ks) {
+                const f16x8 a = *reinterpret_cast<const f16x8*>(xs + ks * 1024 + arow * 64 + kg * 16);
+                const uint8_t* wk = ws + ks * 32 * Epad * 2;
+#pragma unroll
+                for (int b = 0; b < EB; ++b) {
+                    const s16x4 lo = lds_read_tr16(wk + frag_off[0][b]);
+                    const s16x4 hi = lds_read_tr16(wk + frag_off[1][b]);
+                    const f16x8 bv = __builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+                    acc[b] = mfma16x16x32(a, bv, acc[b]);
+                }
+            }
+        }
+        if (j < 3) {
 #pragma unroll
             for (int b = 0; b < EB; ++b) {
-                const s16x4 lo = lds_read_tr16(wk + frag_off[0][b]);
-                const s16x4 hi = lds_read_tr16(wk + frag_off[1][b]);
-                const f16x8 bv = __builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-                acc[b] = mfma16x16x32(a, bv, acc[b]);
+                qsum[b] = j == 0 ? acc[b] : qsum[b] + acc[b];
+                acc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
             }
         }
     }
+#pragma unroll
+    for (int b = 0; b < EB; ++b) acc[b] = qsum[b] + acc[b];  // + q3
     // ---- selection from the accumulators: round r routes token 4 kg + r of each DPP row ----
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -761,6 +787,140 @@ __global__ __launch_bounds__(kRowWaves * kWave) void routing_rows_kernel(const u
         rank_slots<kRowWaves, MAXIT>(expert_ids, t0 * K, min(T, t0 + kRowTokens) * K, E, counts_stride(E),
                                      reinterpret_cast<int*>(lds),
                                      counts + static_cast<size_t>(blockIdx.x) * counts_stride(E), rank);
+    }
+}
+
+// ---- the quarters kernel: one 16-token block per workgroup, wave j sums quarter j of the stages ----
+// With few tokens the rows kernel's 64-token workgroups leave most CUs idle and every wave multiplies all of
+// w_gate. Here a workgroup owns 16 tokens and each of its 4 waves streams one quarter of the stages through
+// double-buffered stages of its own (w_gate 16 KB, x SK KB), with no barrier in the loop: a wave reads only what
+// its own copies wrote. The compiler waits for every direct-to-LDS copy in flight (vmcnt(0)) before a
+// ds_read_b64_tr_b16 that follows it, since it cannot tell which LDS bytes a copy writes, so a stage is read
+// whole into registers before the next stage's copies go out; those then land while the stage's MFMAs run.
+// Wave 0 then adds the other waves' sums in quarter order, ((q0 + q1) + q2) + q3 as the rows kernel does, and
+// selects.
+constexpr size_t quarter_lds_bytes(int eb) { return 4 * (2 * size_t(16384) + 2 * size_t(row_stage_ksteps(eb)) * 1024); }
+
+template <int EB>
+__global__ __launch_bounds__(4 * kWave) void routing_quarters_kernel(const uint16_t* __restrict__ x,
+                                                                     const uint16_t* __restrict__ w_gate,
+                                                                     int32_t* __restrict__ expert_ids,
+                                                                     uint16_t* __restrict__ weights, int T, int H,
+                                                                     int E, int K, int32_t* __restrict__ counts,
+                                                                     int32_t* __restrict__ rank) {
+    constexpr int Epad = EB * 16;
+    constexpr int SK = row_stage_ksteps(EB);
+    constexpr int kStage = SK * 32 * Epad * 2;
+    constexpr int kWaveLds = 2 * kStage + 2 * SK * 1024;
+    static_assert(kStage == 16384, "stage geometry");
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int lane = lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+    uint8_t* wbuf = lds + wave * kWaveLds;  // [2][kStage]
+    uint8_t* xbuf = wbuf + 2 * kStage;       // [2][SK][16 rows][64 B]
+    const int t0 = static_cast<int>(blockIdx.x) * 16;
+    const int nst = H / 32 / SK;  // the host runs this kernel only when SK divides H / 32
+    const int s0 = quarter_begin(wave, nst);
+    const int n = quarter_begin(wave + 1, nst) - s0;  // this wave's stages: s0 .. s0 + n - 1
+
+    const __amdgpu_buffer_rsrc_t wrs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(w_gate), 0, H * E * 2, 0x00020000);
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(x + static_cast<size_t>(t0) * H), 0, min(16, T - t0) * H * 2, 0x00020000);
+    // x copy: lane -> row lane / 4 (token t0 + row, clamped into the batch), 16-byte chunk lane % 4
+    const int xoff = (min(lane / 4, T - 1 - t0) * H + (lane % 4) * 8) * 2;
+    // w_gate copy: the wave fills all 16 slabs of 1 KB of its stage; lane -> 16-byte slot of the slab
+    int woff[16];
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+        const int off = m * 1024 + lane * 16;
+        const int R = off / (32 * EB), pc = (off % (32 * EB)) / 16;  // stage row (SK k-steps of 32), slot
+        const int c = pc ^ ((R % 32) & (2 * EB - 1));                 // the logical chunk stored in slot pc
+        woff[m] = (R * E + (c * 8 < E ? c * 8 : 0)) * 2;              // padding chunks copy any valid chunk
+    }
+    const int arow = lane & 15, kg = lane >> 4;
+    int frag_off[2][EB];
+    {
+        const int sl = lane & 15;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int b = 0; b < EB; ++b) {
+                const int r = 8 * kg + 4 * h + sl / 4;
+                const int e = 16 * b + 4 * (sl % 4);
+                frag_off[h][b] = wstage_chunk<EB>(r, e / 8) + (e % 8) * 2;
+            }
+    }
+    auto issue = [&](int l) __attribute__((always_inline)) {  // this wave's stage s0 + l
+        uint8_t* dst = wbuf + (l & 1) * kStage;
+#pragma unroll
+        for (int m = 0; m < 16; ++m)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (__attribute__((address_space(3))) void*)(dst + m * 1024), 16,
+                                                     static_cast<int>(woff[m]), (s0 + l) * SK * 32 * E * 2, 0, 0);
+#pragma unroll
+        for (int ks = 0; ks < SK; ++ks)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (__attribute__((address_space(3))) void*)(xbuf + ((l & 1) * SK + ks) * 1024),
+                                                     16, xoff, ((s0 + l) * SK + ks) * 64, 0, 0);
+    };
+
+    f32x4 acc[EB];
+#pragma unroll
+    for (int b = 0; b < EB; ++b) acc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (n > 0) issue(0);
+    for (int l = 0; l < n; ++l) {
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // this wave's copies of stage l (the only ones in flight)
+        const uint8_t* ws = wbuf + (l & 1) * kStage;
+        const uint8_t* xs = xbuf + (l & 1) * SK * 1024;
+        f16x8 a[SK], bv[SK][EB];
+#pragma unroll
+        for (int ks = 0; ks < SK; ++ks) {
+            a[ks] = *reinterpret_cast<const f16x8*>(xs + ks * 1024 + arow * 64 + kg * 16);
+            const uint8_t* wk = ws + ks * 32 * Epad * 2;
+#pragma unroll
+            for (int b = 0; b < EB; ++b) {
+                const s16x4 lo = lds_read_tr16(wk + frag_off[0][b]);
+                const s16x4 hi = lds_read_tr16(wk + frag_off[1][b]);
+                bv[ks][b] = __builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+            }
+        }
+        // stage l + 1 refills the buffers of stage l - 1, whose reads fed MFMAs in the previous iteration
+        if (l + 1 < n) issue(l + 1);
+#pragma unroll
+        for (int ks = 0; ks < SK; ++ks)
+#pragma unroll
+            for (int b = 0; b < EB; ++b) acc[b] = mfma16x16x32(a[ks], bv[ks][b], acc[b]);
+    }
+    // waves 1-3 park their quarter sums in their own (idle) w_gate buffers: lane-major f32x4 per expert block
+    if (wave > 0) {
+#pragma unroll
+        for (int b = 0; b < EB; ++b) *reinterpret_cast<f32x4*>(wbuf + (b * kWave + lane) * 16) = acc[b];
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+        for (int j = 1; j < 4; ++j)
+#pragma unroll
+            for (int b = 0; b < EB; ++b)
+                acc[b] = acc[b] + *reinterpret_cast<const f32x4*>(lds + j * kWaveLds + (b * kWave + lane) * 16);
+        // ---- selection from the sums: round r routes token 4 kg + r of each DPP row ----
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float v[EB];
+#pragma unroll
+            for (int b = 0; b < EB; ++b) v[b] = acc[b][r];
+            const int t = t0 + 4 * kg + r;
+            const bool active = t < T;
+            const int tr = active ? t : 0;
+            select_vals<EB>(v, E, K, active, expert_ids + static_cast<size_t>(tr) * K,
+                            weights + static_cast<size_t>(tr) * K);
+        }
+    }
+    // ---- optional tail: the block's slots ranked by expert, for the permute's scatter ----
+    if (counts != nullptr) {
+        __syncthreads();  // the block's ids are written and the sums are no longer read
+        constexpr int MAXIT = (16 * kRankTopK + 4 * kWave - 1) / (4 * kWave);
+        rank_slots<4, MAXIT>(expert_ids, t0 * K, min(T, t0 + 16) * K, E, counts_stride(E), reinterpret_cast<int*>(lds),
+                             counts + static_cast<size_t>(blockIdx.x) * counts_stride(E), rank);
     }
 }
 
@@ -832,6 +992,19 @@ hipError_t launch_eb(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, ui
 }
 
 template <int EB>
+hipError_t launch_quarters(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H, int E,
+                           int K, int32_t* counts, int32_t* rank, hipStream_t stream) {
+    const int grid = (T + 15) / 16;
+    const size_t lds = quarter_lds_bytes(EB);
+    const hipError_t attr = ensure_lds_limit(reinterpret_cast<const void*>(&routing_quarters_kernel<EB>),
+                                             static_cast<int>(lds));
+    if (attr != hipSuccess) return attr;
+    TraceScope trace("moe_routing_topk", stream);
+    routing_quarters_kernel<EB><<<grid, 4 * kWave, lds, stream>>>(x, w_gate, ids, w, T, H, E, K, counts, rank);
+    return hipGetLastError();
+}
+
+template <int EB>
 hipError_t launch_rows(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H, int E,
                        int K, int32_t* counts, int32_t* rank, hipStream_t stream) {
     const int grid = (T + kRowTokens - 1) / kRowTokens;
@@ -847,13 +1020,21 @@ hipError_t launch_rows(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, 
 // Which kernel routes: the narrow kernel for E <= 64; for E > 64 the rows kernel when its copies can run (lw:
 // w_gate rows can be copied 16 bytes at a time, and whole stages of k-steps), else the wide kernel. The choice
 // does not depend on T, so a token's ids and weights do not depend on the batch it is routed in.
-enum RoutingKernel { kNarrowKernel, kWideKernel, kRowsKernel };
+enum RoutingKernel { kNarrowKernel, kWideKernel, kRowsKernel, kQuartersKernel };
+// Tokens up to which the quarters kernel runs instead of the rows kernel (same bits). The rows kernel takes about
+// the same time from T = 128 to 16384 (one workgroup per CU at most, each streaming all of w_gate): 215.6, 75.8,
+// 66.5 and 39.0 us at T = 16384 for the four shapes below. The quarters kernel (us):
+//   E = 256, H = 7168, K = 8: T = 128 46.9, 8192 113.8, 12288 167.0, 16384 220.6
+//   E = 256, H = 2048, K = 8: T = 4096 30.7, 8192 58.9, 12288 86.0, 16384 113.0
+//   E = 128, H = 4096, K = 8: T = 8192 47.0, 12288 69.3, 16384 91.0
+//   E = 128, H = 2048, K = 6: T = 8192 32.0, 12288 46.6, 16384 61.7
+constexpr int64_t kQuartersMaxTokens = 8192;
 RoutingKernel routing_kernel(int T, int H, int E, bool lw) {
-    (void)T;
     const int eb = routing_expert_blocks(E);
     if (eb <= 4) return kNarrowKernel;
     const bool rows_ok = lw && (H / 32) % row_stage_ksteps(eb) == 0;
-    return rows_ok ? kRowsKernel : kWideKernel;
+    if (!rows_ok) return kWideKernel;
+    return T <= kQuartersMaxTokens ? kQuartersKernel : kRowsKernel;
 }
 
 }  // namespace
@@ -873,6 +1054,7 @@ int routing_tokens_per_block(int T, int H, int E, bool lw) {
     const int eb = routing_expert_blocks(E);
     switch (routing_kernel(T, H, E, lw)) {
         case kRowsKernel: return kRowTokens;
+        case kQuartersKernel: return 16;
         case kWideKernel: return kWideTokens;
         default: return kTokensPerBlock * narrow_token_blocks(T, eb);
     }
@@ -881,6 +1063,7 @@ int routing_block_threads(int T, int H, int E, bool lw) {
     const int eb = routing_expert_blocks(E);
     switch (routing_kernel(T, H, E, lw)) {
         case kRowsKernel: return kRowWaves * kWave;
+        case kQuartersKernel: return 4 * kWave;
         case kWideKernel: return kWideWaves * kWave;
         default: return waves_for(eb, narrow_token_blocks(T, eb)) * kWave;
     }
@@ -889,6 +1072,7 @@ int routing_lds_bytes(int T, int H, int E, bool lw) {
     const int eb = routing_expert_blocks(E);
     switch (routing_kernel(T, H, E, lw)) {
         case kRowsKernel: return static_cast<int>(row_lds_bytes(eb));
+        case kQuartersKernel: return static_cast<int>(quarter_lds_bytes(eb));
         case kWideKernel: return static_cast<int>(wide_lds_bytes(eb));
         default: return static_cast<int>(narrow_lds_bytes(eb, narrow_token_blocks(T, eb), lw));
     }
@@ -901,9 +1085,14 @@ int routing_blocks(int T, int H, int E, bool lw) {
 hipError_t launch_routing_topk(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H,
                                int E, int K, hipStream_t stream, int32_t* counts, int32_t* rank) {
     const int eb = routing_expert_blocks(E);
-    if (routing_kernel(T, H, E, narrow_lds_weights(w_gate, H, E)) == kRowsKernel) {
-        return eb == 8 ? launch_rows<8>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream)
-                       : launch_rows<16>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);
+    switch (routing_kernel(T, H, E, narrow_lds_weights(w_gate, H, E))) {
+        case kRowsKernel:
+            return eb == 8 ? launch_rows<8>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream)
+                           : launch_rows<16>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);
+        case kQuartersKernel:
+            return eb == 8 ? launch_quarters<8>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream)
+                           : launch_quarters<16>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);
+        default: break;
     }
     switch (eb) {
         case 1: return launch_eb<1>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);

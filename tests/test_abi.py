@@ -113,6 +113,12 @@ def test_plans(lib):
     assert lib.moe_routing_topk_plan(16384, 2048, 256, 8, C.byref(rp)) == MOE_OK
     assert (rp.grid, rp.block, rp.tokens_per_block) == (256, 256, 64)
     assert rp.lds_bytes == 4 * 16384 + 4 * (16 + 1) * 1024  # the rows kernel: 4 w_gate stages, x rings
+    # E > 64 and T <= 8192: 16 tokens per workgroup; the quarters kernel (4 waves, each a quarter of H through two
+    # 16 KB w_gate stages and two 1 KB x stages of its own)
+    assert lib.moe_routing_topk_plan(128, 7168, 256, 8, C.byref(rp)) == MOE_OK
+    assert (rp.grid, rp.block, rp.tokens_per_block, rp.lds_bytes) == (8, 256, 16, 4 * (2 * 16384 + 2 * 1024))
+    assert lib.moe_routing_topk_plan(8192, 2048, 128, 8, C.byref(rp)) == MOE_OK
+    assert (rp.grid, rp.block, rp.tokens_per_block, rp.lds_bytes) == (512, 256, 16, 4 * (2 * 16384 + 2 * 2 * 1024))
     # E % 8 != 0 (no 16-byte w_gate rows): the wide kernel, w_gate transposed through LDS
     assert lib.moe_routing_topk_plan(16384, 2048, 250, 8, C.byref(rp)) == MOE_OK
     assert (rp.grid, rp.block, rp.tokens_per_block) == (256, 256, 64)

@@ -319,6 +319,29 @@ def test_routing_is_batch_invariant(ops, E, K):
     assert np.array_equal(host(w_all)[:1000].view(np.uint16), host(w_few).view(np.uint16))
 
 
+@pytest.mark.parametrize("H,E,K", [
+    (7168, 256, 8),  # DeepSeek-V3's routing: 224 stages, 56 a quarter
+    (2048, 128, 6),  # two k-steps a stage (E = 128): 32 stages
+    (160, 256, 4),   # 5 stages: quarters of 1, 1, 1 and 2 stages
+    (128, 128, 2),   # 2 stages: quarters 0 and 2 empty
+])
+def test_routing_quarters_and_rows_kernels_agree(ops, H, E, K):
+    """E > 64: up to 8192 tokens the quarters kernel routes (16 tokens a workgroup, a wave per quarter of H), above
+    that the rows kernel (64 tokens a workgroup, the quarters one after the other in each wave). Both add a token's
+    H in the same four quarter sums, so 8300 tokens routed together and their first 1000 routed alone agree bit for
+    bit; the small batch is also checked against the oracle's routing."""
+    T = 8300
+    rng = np.random.default_rng(H + E)
+    x = rng.standard_normal((T, H)).astype(np.float16)
+    wg = (rng.standard_normal((H, E)) / math.sqrt(H)).astype(np.float16)
+    ids_all, w_all = ops.MoeRoutingTopK(dev(x), dev(wg), K)
+    ids_few, w_few = ops.MoeRoutingTopK(dev(x[:1000]), dev(wg), K)
+    ids_few, w_few = host(ids_few), host(w_few)
+    assert np.array_equal(host(ids_all)[:1000], ids_few)
+    assert np.array_equal(host(w_all)[:1000].view(np.uint16), w_few.view(np.uint16))
+    check_routing(ids_few, w_few, x[:1000], wg, K, f"quarters H{H} E{E} K{K}")
+
+
 def test_routing_rows_kernel_past_2gib_of_x(ops):
     """E > 64 with x past 2 GiB (T = 2^19 + 80, H = 2048): the rows kernel addresses each workgroup's own x rows,
     so it still runs and a token's ids and weights are the same bits as when its workgroup's tokens are routed
@@ -1131,6 +1154,8 @@ def test_concurrent_threads_and_streams(ops):
     (3000, 128, 130, 4, 128, 1),   # E > 64: the wide routing kernel counts its 64 tokens
     (300, 128, 48, 40, 128, 1),    # K = 40: a block's 640 slots are ranked in two passes
     (1000, 128, 100, 64, 128, 1),  # wide kernel, K = 64: 4096 slots per block, two passes
+    (4096, 256, 128, 8, 128, 1),   # E = 128, T <= 8192: the quarters kernel ranks its 16-token blocks
+    (9000, 256, 128, 4, 128, 1),   # E = 128, T > 8192: the rows kernel ranks its 64-token blocks
 ])
 def test_fused_layer_matches_oracle_and_operators(ops, T, H, E, K, I, schedule):
     """moe_layer (routing that also ranks its blocks' slots, one scatter launch, the FFN, the combine): ids and
