@@ -39,7 +39,9 @@
 //      block; per block: the four whole-line loads go through the wave's LDS re-layout buffer, activation
 //      fragments come from the LDS stage (ds_read_b128), v_mfma_f32_16x16x32_f16 (fp32 accumulation).
 //      With kc = 32 (D = 1) the loads go straight into the MFMA order instead (register ring of D k-steps);
-//   4. epilogue in registers: gate/up -> hidden = silu(gate) * up (fp32) -> fp16 workspace row;
+//   4. epilogue in registers: gate/up -> hidden = silu(gate) * up (fp32) -> fp16 workspace row; gate/up over
+//      several K-ranges (an H whose 32 rows do not fit LDS whole) -> fp32 gate and up partial sums, which
+//      gateup_reduce_kernel adds in K-range order before the SwiGLU;
 //      down with one K-range -> expert_out[slot] fp16 (the scatter back to [T, K, H] order);
 //      down with several K-ranges -> fp32 partial sums, added in a fixed order by down_reduce_kernel (no atomics,
 //      deterministic). Letting the last of the nsplit workgroups of an (expert, column group) add them instead
@@ -82,8 +84,8 @@ struct StreamArgs {
     const int32_t* sorted_slot;   // [T*K]
     const int32_t* offsets;       // [E+1]
     const uint16_t* w;            // expert_weights [E, 3I, H]
-    uint16_t* out;                // hidden (kSwiGLU) or expert_out (kScatter)
-    float* partial;               // [nsplit][T*K][H] fp32 (kPartial)
+    uint16_t* out;                // hidden (kSwiGLU) or expert_out (kScatter); unused by the partial epilogues
+    float* partial;               // fp32 [nsplit][T*K][H] (kPartial) or [nsplit][T*K][2I] (kGatePartial)
     int E, K, H, I;
     int kdim;                     // reduction extent: H (gate/up) or I (down)
     int ndim;                     // output columns: I (gate/up) or H (down)
@@ -837,14 +839,18 @@ StreamShape pick_shape(int kdim, bool allow_split) {
 // 2272), each unit covers one K-range of H at 32 rows instead and writes fp32 gate and up sums (kGatePartial),
 // which gateup_reduce_kernel adds before the SwiGLU: one more launch and 2 * nsplit * 4 bytes per (row, i) of
 // traffic, where the whole-H layout holds 16 rows (an expert with more rows re-streams its weights per 16 rows;
-// up to H = 4568) or none at all. K-ranges are multiples of 256 (the deepest ring): at H = 2336 the only split
-// is 73 K-ranges of 32, and the FFN took 473.5 us against 183.3 us unsplit (T = 64, E = 16, K = 2, I = 4096).
+// up to H = 4568) or none at all. The K-range is the largest multiple of 32 D dividing H, deepest ring first, and at
+// least 256 columns: at H = 2336 the only split is 73 K-ranges of 32, and the FFN took 473.5 us against 183.3 us
+// unsplit (T = 64, E = 16, K = 2, I = 4096).
 StreamShape gateup_split_shape(int H) {
     const int kc_max = (kLdsMax - kTbBytes) / (kMaxRows * 2) - 8;
-    int best = 0;
-    for (int kc = 256; kc <= kc_max && kc <= H; kc += 256)
-        if (H % kc == 0) best = kc;
-    return best > 0 ? StreamShape{best, 8, kMaxRows, H / best} : StreamShape{0, 0, 0, 0};
+    for (int d = 8; d >= 1; d /= 2) {
+        int best = 0;
+        for (int kc = 32 * d; kc <= kc_max && kc <= H; kc += 32 * d)
+            if (H % kc == 0 && kc >= 256) best = kc;
+        if (best > 0) return StreamShape{best, d, kMaxRows, H / best};
+    }
+    return StreamShape{0, 0, 0, 0};
 }
 // Average rows per expert from which the 32-row kernel splits an H that 16 rows fit whole: below it one 16-row
 // pass covers most experts and the partial sums are extra traffic. The FFN at E = 16, K = 2, I = 4096, 16-row

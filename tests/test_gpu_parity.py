@@ -1205,38 +1205,41 @@ def random_shapes(n: int, seed: int):
     return shapes
 
 
-def test_random_shape_sweep(ops):
-    """Seeded random shapes through the three operators and through moe_layer, every token checked: ids and
-    weights against the oracle's routing, expert_out against the oracle FFN of the same ids, y bit for bit against
-    the oracle's combine of that expert_out, and moe_layer equal to the three operators bit for bit. Shapes the
-    planner rejects must be rejected with MOE_ERR_UNSUPPORTED; the sweep must reach both FFN schedules."""
+def run_shape_sweep(ops, shapes, tag):
+    """Each shape through the three operators and through moe_layer, every token checked: ids and weights against
+    the oracle's routing, expert_out against the oracle FFN of the same ids, y bit for bit against the oracle's
+    combine of that expert_out, and moe_layer equal to the three operators bit for bit. Shapes the planner rejects
+    must be rejected with MOE_ERR_UNSUPPORTED. Returns the number of shapes per FFN schedule and the number whose
+    gate/up splits H over K-ranges (the plan's gate/up grid above E x ceil(I / 128) on the streaming schedule)."""
     import ctypes as C
 
     from conftest import package
 
     lib_mod = package()._lib
     lib = lib_mod.load()
-    seen = {0: 0, 1: 0}
-    for n, (T, H, E, K, I) in enumerate(random_shapes(24, 2026)):
+    seen = {0: 0, 1: 0, "gateup_split": 0}
+    for n, (T, H, E, K, I) in enumerate(shapes):
         plan = lib_mod.FfnPlan()
         st = lib.moe_expert_ffn_plan(T, H, E, K, I, C.byref(plan))
         if st != 0:
             assert lib_mod.STATUS_NAMES.get(st) == "MOE_ERR_UNSUPPORTED", (T, H, E, K, I, st)
-            log(f"[sweep {n}] T={T} H={H} E={E} K={K} I={I}: unsupported ({lib.moe_last_error().decode()})")
+            log(f"[{tag} {n}] T={T} H={H} E={E} K={K} I={I}: unsupported ({lib.moe_last_error().decode()})")
             continue
         seen[plan.schedule] += 1
+        split = plan.schedule == 0 and plan.gateup_grid > E * ((I + 127) // 128)
+        seen["gateup_split"] += int(split)
         rng = np.random.default_rng(n)
-        x = rng.standard_normal((T, H)).astype(np.float16)
-        wg = (rng.standard_normal((H, E)) / math.sqrt(H)).astype(np.float16)
-        ew = np.concatenate([rng.standard_normal((E, 2 * I, H)) / math.sqrt(H),
-                             rng.standard_normal((E, I, H)) / math.sqrt(I)], axis=1).astype(np.float16)
+        x = rng.standard_normal((T, H), dtype=np.float32).astype(np.float16)
+        wg = (rng.standard_normal((H, E), dtype=np.float32) / math.sqrt(H)).astype(np.float16)
+        ew = np.concatenate([rng.standard_normal((E, 2 * I, H), dtype=np.float32) / math.sqrt(H),
+                             rng.standard_normal((E, I, H), dtype=np.float32) / math.sqrt(I)], axis=1).astype(np.float16)
         x_d, wg_d, ew_d = dev(x), dev(wg), dev(ew)
         ids_d, w_d = ops.MoeRoutingTopK(x_d, wg_d, K)
         eo_d = ops.MoeExpertFFN(x_d, ids_d, w_d, ew_d)
         y_d = ops.MoeCombine(eo_d, ids_d, w_d, K)
         ids, w = host(ids_d), host(w_d)
-        log(f"[sweep {n}] T={T} H={H} E={E} K={K} I={I} schedule={plan.schedule} rows/tile={plan.rows_per_tile}")
-        check_routing(ids, w, x, wg, K, f"sweep {n}")
+        log(f"[{tag} {n}] T={T} H={H} E={E} K={K} I={I} schedule={plan.schedule} gate/up split={split}")
+        check_routing(ids, w, x, wg, K, f"{tag} {n}")
         eo = f32(host(eo_d))
         within(oracle.compare(eo, oracle_ffn_threads(f32(x), ids, f32(ew), I)), max_abs=1e-2, mean_abs=1e-3,
                cos=0.9999)
@@ -1245,8 +1248,37 @@ def test_random_shape_sweep(ops):
         layer = ops.moe_layer(x_d, wg_d, ew_d, K)
         for name, a, b in zip(("y", "ids", "weights", "expert_out"), layer, (y_d, ids_d, w_d, eo_d)):
             assert torch.equal(a, b), (name, n)
-    log(f"[sweep] shapes per schedule: {seen}")
+    log(f"[{tag}] shapes per schedule: {seen}")
+    return seen
+
+
+def test_random_shape_sweep(ops):
+    """24 seeded random shapes (H, I <= 768) through run_shape_sweep; the sweep must reach both FFN schedules."""
+    seen = run_shape_sweep(ops, random_shapes(24, 2026), "sweep")
     assert seen[0] >= 3 and seen[1] >= 3, seen
+
+
+def random_long_hidden_shapes(n: int, seed: int):
+    """n seeded shapes with H from 2304 to 8192 (multiples of 32; above 2272 the 32-row gate/up kernel splits H),
+    E up to 256 (every routing kernel), expert weights up to 2e8 elements and the oracle FFN near 2e9 multiply-adds
+    per shape, so T stays small and most shapes take the streaming schedule."""
+    rng = np.random.default_rng(seed)
+    shapes = []
+    while len(shapes) < n:
+        H = 32 * int(rng.integers(72, 257))
+        I = 32 * int(rng.integers(1, 25))
+        E = int(rng.integers(1, min(256, int(2e8 // (3 * I * H))) + 1))
+        K = int(rng.integers(1, min(E, 8) + 1))
+        T = int(rng.integers(1, max(1, min(600, int(2e9 // (3 * K * H * I)))) + 1))
+        shapes.append((T, H, E, K, I))
+    return shapes
+
+
+def test_random_long_hidden_sweep(ops):
+    """12 seeded random shapes with a long H through run_shape_sweep: the 32-row gate/up kernel's K-range split
+    must be reached."""
+    seen = run_shape_sweep(ops, random_long_hidden_shapes(12, 7168), "long-H sweep")
+    assert seen["gateup_split"] >= 2, seen
 
 
 def test_decode_uses_streaming_and_prefill_uses_tiled():
