@@ -20,6 +20,9 @@
 //            renormalisation with all-reduces over the token's lanes (select_row): max,
 //            expf(l - max), sum, division by the sum; K rounds of an arg-max (lowest index wins an exact tie); the
 //            renormalising sum over the K picks in rank order; fp16 round-to-nearest-even.
+// From 32768 tokens, for 32 < E <= 64 (H a multiple of 1024), the resident kernel replaces the narrow one with the
+// same bits: one workgroup per CU holds the narrow kernel's w_gate fragments in registers and streams x through
+// an LDS ring, so w_gate is read once per CU instead of once per 32 tokens.
 // For E > 64 the rows kernel runs above 8192 tokens: a workgroup owns 64 tokens and each of its 4 waves 16 of them
 // over all of H, so the selection runs on the accumulators. w_gate stages (16 KB, row-major) are copied into LDS
 // with 16-byte direct-to-LDS loads and shared by the 4 waves; each wave's x rows stream through its own LDS ring
@@ -924,6 +927,254 @@ __global__ __launch_bounds__(4 * kWave) void routing_quarters_kernel(const uint1
     }
 }
 
+// ---- resident kernel: E <= 64 at large T, w_gate held in registers ----
+// The narrow kernel's workgroups each route 16-64 tokens and multiply all of w_gate into them, so at T = 16384,
+// E = 64 they read 128 MB of w_gate from L2 beside 64 MB of x, four dependent round trips a wave. This kernel is
+// persistent (one workgroup per CU, a contiguous run of 16-token blocks each) and reads w_gate once per
+// workgroup: its 8 waves hold every B fragment of the narrow kernel in VGPRs. x streams through an LDS ring of
+// 32 KB slots (16 token rows x 1024 columns), copied straight from memory into LDS a few slots ahead.
+// Same bits as the narrow kernel: the narrow kernel's W waves are kept as virtual waves v (wave v's k-step pairs
+// v, v + W, ..., each pair's two k-steps in order, on the same MFMA chain), each physical wave runs VPW virtual
+// waves for BPW of the EB expert blocks, and the W partials are folded in virtual-wave order before the same
+// selection. Fragments are read from the narrow kernel's w_gate stage layout (wstage_chunk, ds_read_b64_tr_b16).
+// LDS of a ring slot: token row r at r * 2048 bytes; 16-byte granule g of the row at g ^ r, so the 16 rows an
+// A-fragment read touches lie in distinct banks.
+constexpr int kResWaves = 8;
+constexpr int kResChunk = 1024;                                  // x columns per ring slot (32 k-steps)
+constexpr int kResSlotBytes = 16 * kResChunk * 2;                // 32 KB
+constexpr int kResCopies = kResSlotBytes / 1024 / kResWaves;     // 1 KB copies per wave and slot: 4
+constexpr int res_slots(int eb) { return eb == 2 ? 3 : 4; }      // with the partials, within 160 KB of LDS
+constexpr int res_vw(int eb) { return waves_for(eb, 1); }       // the narrow kernel's waves
+constexpr int res_vpw(int eb) { return res_vw(eb) >= kResWaves ? res_vw(eb) / kResWaves : 1; }
+constexpr int res_bpw(int eb) { return eb * res_vw(eb) / kResWaves / res_vpw(eb); }
+// B fragments a wave holds for NPV pairs per virtual wave (H = 64 W NPV): at most 32 (128 VGPRs)
+constexpr int res_frags(int eb, int npv) { return res_vpw(eb) * res_bpw(eb) * npv * 2; }
+// Token blocks whose folded logits wait in LDS for one selection round of all 8 waves (16 KB of them)
+constexpr int res_sel_blocks(int eb) { return 16 / eb; }
+constexpr size_t res_lds_bytes(int eb) {
+    return static_cast<size_t>(res_slots(eb)) * kResSlotBytes + static_cast<size_t>(res_vw(eb)) * 16 * eb * 16 * 4 +
+           static_cast<size_t>(res_sel_blocks(eb)) * 16 * eb * 16 * 4;
+}
+// Workgroups of the persistent grid: one per CU of the MI355X.
+constexpr int kResGrid = 256;
+int res_blocks_per_wg(int T) {
+    const int nblocks = (T + 15) / 16;
+    return (nblocks + kResGrid - 1) / kResGrid;
+}
+
+// Barrier over this wave's LDS accesses only: the x copies in flight (vmcnt) are not waited for, as a
+// workgroup-scope release fence would. The LDS writes before it are this wave's ds_writes (lgkmcnt) and the
+// copies of slots the caller waited for explicitly.
+__device__ __forceinline__ void lds_barrier_nowait() {
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// Four ds_read_b64_tr_b16 and their wait as one inline-assembly statement. The compiler waits for every
+// direct-to-LDS copy in flight before the builtin (it cannot tell which LDS bytes a copy writes), which would hold
+// the fragment reads behind the x copies of the ring; here the registers are whole when the statement ends.
+__device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const uint8_t*)(p)));
+}
+__device__ __forceinline__ void lds_read_tr16_x4(const uint8_t* p0, const uint8_t* p1, const uint8_t* p2,
+                                                 const uint8_t* p3, s16x4 (&v)[4]) {
+    asm volatile(
+        "ds_read_b64_tr_b16 %0, %4\n\tds_read_b64_tr_b16 %1, %5\n\tds_read_b64_tr_b16 %2, %6\n\t"
+        "ds_read_b64_tr_b16 %3, %7\n\ts_waitcnt lgkmcnt(0)"
+        : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3])
+        : "v"(lds_addr(p0)), "v"(lds_addr(p1)), "v"(lds_addr(p2)), "v"(lds_addr(p3)));
+}
+
+template <int EB, int NPV, bool NTX>
+__global__ __launch_bounds__(kResWaves * kWave) void routing_resident_kernel(const uint16_t* __restrict__ x,
+                                                                             const uint16_t* __restrict__ w_gate,
+                                                                             int32_t* __restrict__ expert_ids,
+                                                                             uint16_t* __restrict__ weights, int T,
+                                                                             int H, int E, int K, int bpw,
+                                                                             int32_t* __restrict__ counts,
+                                                                             int32_t* __restrict__ rank) {
+    constexpr int VW = res_vw(EB), VPW = res_vpw(EB), BPW = res_bpw(EB);
+    constexpr int Epad = EB * 16;
+    constexpr int R = res_slots(EB);
+    constexpr int PPC = 16 / VW;      // pairs of a virtual wave in one slot (32 k-steps = 16 pairs)
+    constexpr int NCH = NPV / PPC;    // slots per token block: H / kResChunk
+    static_assert(NCH * PPC == NPV && res_frags(EB, NPV) <= 32, "resident geometry");
+    static_assert(BPW == 2, "the fragment reads take two expert blocks at a time");
+    extern __shared__ __align__(16) uint8_t lds[];
+    constexpr int SB = res_sel_blocks(EB);
+    float* part = reinterpret_cast<float*>(lds + R * kResSlotBytes);  // [VW][16 tokens][Epad]
+    float* logit = part + VW * 16 * Epad;                              // [SB][16 tokens][Epad]
+    const int lane = lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+    const int row = lane & 15, kg = lane >> 4;
+    // this wave's virtual waves v0 .. v0 + VPW - 1 and expert blocks b0 .. b0 + BPW - 1
+    const int v0 = VW >= kResWaves ? wave * VPW : wave / (kResWaves / VW);
+    const int b0 = VW >= kResWaves ? 0 : (wave % (kResWaves / VW)) * BPW;
+    const int nblocks = (T + 15) / 16;
+    const int blk0 = static_cast<int>(blockIdx.x) * bpw;  // the host sizes the grid so that blk0 < nblocks
+    const int blk1 = min(nblocks, blk0 + bpw);
+
+    // ---- x ring: copy m of a wave fills 1 KB = half of token row r = 2 wave + m / 2 ----
+    int xoff[kResCopies];
+#pragma unroll
+    for (int m = 0; m < kResCopies; ++m) {
+        const int r = 2 * wave + m / 2;
+        const int lg = (64 * (m & 1) + lane) ^ r;  // the logical granule stored in this lane's physical granule
+        xoff[m] = r * H * 2 + lg * 16;
+    }
+    const int nq = (blk1 - blk0) * NCH;  // ring slots this workgroup runs through
+    auto issue = [&](int qq) __attribute__((always_inline)) {
+        const int b = blk0 + qq / NCH, c = qq % NCH;
+        const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t*>(x + static_cast<size_t>(b) * 16 * H), 0, min(16, T - b * 16) * H * 2, 0x00020000);
+        uint8_t* dst = lds + (qq % R) * kResSlotBytes + wave * kResCopies * 1024;
+#pragma unroll
+        for (int m = 0; m < kResCopies; ++m)  // rows past T read zeros; their results are dropped
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (__attribute__((address_space(3))) void*)(dst + m * 1024), 16,
+                                                     xoff[m], c * kResChunk * 2, 0, NTX ? 2 : 0);
+    };
+    const int nx0 = min(R - 1, nq);  // ring slots issued during the w_gate staging
+
+    // ---- w_gate into registers: k-steps staged 32 rows at a time in the narrow kernel's layout, in the last ring
+    // slot, the partials and the logits, while the x copies of the other slots are in flight ----
+    f16x8 wf[VPW][BPW][NPV][2];
+    {
+        constexpr int kStep = EB * 1024;  // one k-step's 32 rows x Epad, 2 Epad 16-byte chunks a row
+        constexpr int kStaging = static_cast<int>(res_lds_bytes(EB)) - (R - 1) * kResSlotBytes;
+        uint8_t* stage0 = lds + (R - 1) * kResSlotBytes;
+        const int kpp = kStaging / kStep;
+        const int nsteps = H / 32;
+        // copy j fills stage bytes [1024 j, 1024 j + 1024); a wave's copies are j = wave (mod 8), so all of them
+        // are chunk i = wave % EB of their k-step
+        const int slot = (wave % EB) * kWave + lane;
+        const int r = slot / (2 * EB), pc = slot % (2 * EB);
+        const int c = pc ^ (r & (2 * EB - 1));
+        const int cpy = (r * E + (c * 8 < E ? c * 8 : 0)) * 2;  // padding chunks copy any valid chunk
+        int frag_off[2][BPW];
+        const int sl = lane & 15;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int bi = 0; bi < BPW; ++bi) {
+                const int rr = 8 * kg + 4 * h + sl / 4;
+                const int e = 16 * (b0 + bi) + 4 * (sl % 4);
+                frag_off[h][bi] = wstage_chunk<EB>(rr, e / 8) + (e % 8) * 2;
+            }
+        const __amdgpu_buffer_rsrc_t wrs =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(w_gate), 0, H * E * 2, 0x00020000);
+        for (int ks0 = 0; ks0 < nsteps; ks0 += kpp) {
+            const int nks = min(kpp, nsteps - ks0);
+            if (ks0 > 0) lds_barrier_nowait();  // every wave has read the previous pass's stages
+            for (int j = wave; j < nks * EB; j += kResWaves)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (__attribute__((address_space(3))) void*)(stage0 + j * 1024), 16,
+                                                         cpy, (ks0 + j / EB) * 32 * E * 2, 0, 0);
+            if (ks0 == 0) {  // the x slots go out behind the first pass's copies, which are waited for alone
+                for (int qq = 0; qq < nx0; ++qq) issue(qq);
+                if (nx0 >= 3) __builtin_amdgcn_s_waitcnt(vmcnt_imm(3 * kResCopies));
+                else if (nx0 == 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kResCopies));
+                else __builtin_amdgcn_s_waitcnt(vmcnt_imm(kResCopies));
+            } else {
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+            }
+            lds_barrier_nowait();  // (a workgroup release fence would wait for the x copies as well)
+#pragma unroll
+            for (int vi = 0; vi < VPW; ++vi)
+#pragma unroll
+                for (int ii = 0; ii < NPV; ++ii)
+#pragma unroll
+                    for (int st = 0; st < 2; ++st) {
+                        const int ks = 2 * (v0 + vi + ii * VW) + st;
+                        if (ks < ks0 || ks >= ks0 + nks) continue;  // uniform
+                        const uint8_t* stg = stage0 + (ks - ks0) * kStep;
+                        s16x4 v[4];  // halves lo, hi of expert blocks b0, b0 + 1
+                        lds_read_tr16_x4(stg + frag_off[0][0], stg + frag_off[1][0], stg + frag_off[0][1],
+                                         stg + frag_off[1][1], v);
+#pragma unroll
+                        for (int bi = 0; bi < BPW; ++bi)
+                            wf[vi][bi][ii][st] = __builtin_bit_cast(f16x8, __builtin_shufflevector(v[2 * bi], v[2 * bi + 1], 0, 1, 2, 3, 4, 5, 6, 7));
+                    }
+        }
+        lds_barrier_nowait();  // every wave's fragments are in registers before the ring overwrites the stages
+    }
+
+
+    constexpr int G = narrow_sel_lanes(EB);
+    constexpr int TPW = kWave / G;
+    int q = 0;
+    for (int b = blk0; b < blk1; ++b) {
+        f32x4 acc[VPW][BPW];
+#pragma unroll
+        for (int vi = 0; vi < VPW; ++vi)
+#pragma unroll
+            for (int bi = 0; bi < BPW; ++bi) acc[vi][bi] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < NCH; ++c, ++q) {
+            // this wave's copies of slot q have landed (those of up to R - 2 later slots may be in flight) ...
+            const int ahead = min(R - 2, nq - 1 - q);
+            if (ahead >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kResCopies));
+            else if (ahead == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(kResCopies));
+            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+            lds_barrier_nowait();  // its reads of slot q - 1 are done, and every wave's: slot q is whole, q - 1 free
+            if (q + R - 1 < nq) issue(q + R - 1);
+            const uint8_t* xs = lds + (q % R) * kResSlotBytes + row * 2048;
+#pragma unroll
+            for (int vi = 0; vi < VPW; ++vi)
+#pragma unroll
+                for (int ii = c * PPC; ii < (c + 1) * PPC; ++ii)
+#pragma unroll
+                    for (int st = 0; st < 2; ++st) {
+                        const int ksl = 2 * (v0 + vi + ii * VW) + st - 32 * c;  // k-step within the slot
+                        const f16x8 a = *reinterpret_cast<const f16x8*>(xs + (((ksl * 4 + kg) ^ row) << 4));
+#pragma unroll
+                        for (int bi = 0; bi < BPW; ++bi) acc[vi][bi] = mfma16x16x32(a, wf[vi][bi][ii][st], acc[vi][bi]);
+                    }
+        }
+        // partial logits of each virtual wave: D[token 4 kg + r][expert 16 b + row]
+#pragma unroll
+        for (int vi = 0; vi < VPW; ++vi)
+#pragma unroll
+            for (int bi = 0; bi < BPW; ++bi)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    part[((v0 + vi) * 16 + kg * 4 + r) * Epad + (b0 + bi) * 16 + row] = acc[vi][bi][r];
+        lds_barrier_nowait();
+        // fold in virtual-wave order into the block's logits rows
+        const int lb = (b - blk0) % SB;
+        const f32x4* part4 = reinterpret_cast<const f32x4*>(part);
+        f32x4* logit4 = reinterpret_cast<f32x4*>(logit + lb * 16 * Epad);
+        for (int i = static_cast<int>(threadIdx.x); i < 16 * Epad / 4; i += kResWaves * kWave) {
+            f32x4 v = part4[i];
+#pragma unroll
+            for (int w = 1; w < VW; ++w) v += part4[w * 16 * Epad / 4 + i];
+            logit4[i] = v;
+        }
+        // selection of the blocks held, all waves at once: G lanes per token, TPW tokens a wave. The next block's
+        // partials are written after a ring barrier, which every wave reaches after its fold reads.
+        if (lb == SB - 1 || b == blk1 - 1) {
+            lds_barrier_nowait();
+            const int tb0 = (b - lb) * 16;  // the first token of the blocks held
+            const int nt = (lb + 1) * 16;
+            for (int tw = wave * TPW; tw < nt; tw += kResWaves * TPW) {  // uniform: every lane joins the DPP steps
+                const int t = tw + lane / G;
+                const bool active = t < nt && tb0 + t < T;
+                const int tr = min(t, nt - 1);  // inactive groups read a valid row and write nothing
+                select_row<Epad / G, G>(logit + tr * Epad, E, K, active, expert_ids + static_cast<size_t>(tb0 + tr) * K,
+                                        weights + static_cast<size_t>(tb0 + tr) * K);
+            }
+        }
+    }
+    // ---- optional tail: the workgroup's slots ranked by expert, for the permute's scatter ----
+    if (counts != nullptr) {
+        __syncthreads();  // the workgroup's ids are written and part[] is no longer read
+        rank_slots<kResWaves, 4>(expert_ids, blk0 * 16 * K, min(T, blk1 * 16) * K, E, counts_stride(E),
+                                 reinterpret_cast<int*>(part), counts + static_cast<size_t>(blockIdx.x) * counts_stride(E),
+                                 rank);
+    }
+}
+
 size_t wide_lds_bytes(int eb) {
     const int pitch = eb == 8 ? wide_pitch(8) : wide_pitch(16);
     return static_cast<size_t>(2) * eb * 16 * pitch * sizeof(uint16_t) +
@@ -991,6 +1242,61 @@ hipError_t launch_eb(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, ui
     }
 }
 
+template <int EB, int NPV, bool NTX>
+hipError_t launch_resident_nt(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H,
+                              int E, int K, int32_t* counts, int32_t* rank, hipStream_t stream) {
+    const int bpw = res_blocks_per_wg(T);
+    const int grid = ((T + 15) / 16 + bpw - 1) / bpw;
+    const size_t lds = res_lds_bytes(EB);
+    const hipError_t attr = ensure_lds_limit(reinterpret_cast<const void*>(&routing_resident_kernel<EB, NPV, NTX>),
+                                             static_cast<int>(lds));
+    if (attr != hipSuccess) return attr;
+    TraceScope trace("moe_routing_topk", stream);
+    routing_resident_kernel<EB, NPV, NTX><<<grid, kResWaves * kWave, lds, stream>>>(x, w_gate, ids, w, T, H, E, K, bpw,
+                                                                                     counts, rank);
+    return hipGetLastError();
+}
+
+template <int EB, int NPV>
+hipError_t launch_resident(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H, int E,
+                           int K, int32_t* counts, int32_t* rank, hipStream_t stream) {
+    if (static_cast<int64_t>(T) * H * 2 >= kNtXBytes)
+        return launch_resident_nt<EB, NPV, true>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);
+    return launch_resident_nt<EB, NPV, false>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);
+}
+
+// pairs per virtual wave of the resident kernel for this shape, or 0 where it does not run (H a multiple of
+// 1024 and of 64 W, the fragments within 128 VGPRs, an instantiated NPV)
+int resident_npv(int H, int eb) {
+    if (eb != 4 || H % kResChunk != 0) return 0;
+    const int vw = res_vw(eb);
+    if (H % (64 * vw) != 0) return 0;
+    const int npv = H / (64 * vw);
+    if (npv != 2 && npv != 4 && npv != 8) return 0;
+    return res_frags(eb, npv) <= 32 ? npv : 0;
+}
+
+template <int EB>
+hipError_t launch_resident_eb(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H,
+                              int E, int K, int32_t* counts, int32_t* rank, hipStream_t stream) {
+    switch (resident_npv(H, EB)) {
+        case 2:
+            if constexpr (res_frags(EB, 2) <= 32 && (2 * res_vw(EB)) % 16 == 0)
+                return launch_resident<EB, 2>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);
+            break;
+        case 4:
+            if constexpr (res_frags(EB, 4) <= 32 && (4 * res_vw(EB)) % 16 == 0)
+                return launch_resident<EB, 4>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);
+            break;
+        case 8:
+            if constexpr (res_frags(EB, 8) <= 32 && (8 * res_vw(EB)) % 16 == 0)
+                return launch_resident<EB, 8>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);
+            break;
+        default: break;
+    }
+    return hipErrorInvalidValue;
+}
+
 template <int EB>
 hipError_t launch_quarters(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H, int E,
                            int K, int32_t* counts, int32_t* rank, hipStream_t stream) {
@@ -1020,7 +1326,7 @@ hipError_t launch_rows(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, 
 // Which kernel routes: the narrow kernel for E <= 64; for E > 64 the rows kernel when its copies can run (lw:
 // w_gate rows can be copied 16 bytes at a time, and whole stages of k-steps), else the wide kernel. The choice
 // does not depend on T, so a token's ids and weights do not depend on the batch it is routed in.
-enum RoutingKernel { kNarrowKernel, kWideKernel, kRowsKernel, kQuartersKernel };
+enum RoutingKernel { kNarrowKernel, kWideKernel, kRowsKernel, kQuartersKernel, kResidentKernel };
 // Tokens up to which the quarters kernel runs instead of the rows kernel (same bits). The rows kernel takes about
 // the same time from T = 128 to 16384 (one workgroup per CU at most, each streaming all of w_gate): 215.6, 75.8,
 // 66.5 and 39.0 us at T = 16384 for the four shapes below. The quarters kernel (us):
@@ -1029,9 +1335,19 @@ enum RoutingKernel { kNarrowKernel, kWideKernel, kRowsKernel, kQuartersKernel };
 //   E = 128, H = 4096, K = 8: T = 8192 47.0, 12288 69.3, 16384 91.0
 //   E = 128, H = 2048, K = 6: T = 8192 32.0, 12288 46.6, 16384 61.7
 constexpr int64_t kQuartersMaxTokens = 8192;
+// Tokens from which 32 < E <= 64 routes through the resident kernel (same bits as the narrow kernel). Isolated
+// launches at H = 2048, E = 64, K = 6, x streamed from HBM (non-temporal) / evicted first, us:
+//   T =  4096: narrow 12.2 / 14.9,  resident 13.6 / 17.8
+//   T =  8192: narrow 14.1 / 17.9,  resident 15.5 / 20.8
+//   T = 16384: narrow 22.5 / 24.9,  resident 20.8 / 25.7  (in the DeepSeek-V2-Lite layer 23.3 against 24.1-24.4)
+//   T = 32768: narrow 39.3 / 41.4,  resident 32.6 / 37.7
+// Each CU stages all of w_gate once (256 KB through LDS, ~3-4 us, partly behind the first x slots) and selects its
+// tokens at the end, where the narrow kernel's two workgroups per CU hide one's selection behind the other's
+// loads: the resident kernel gains only once a CU routes 128 tokens or more.
+constexpr int64_t kResidentMinTokens = 32768;
 RoutingKernel routing_kernel(int T, int H, int E, bool lw) {
     const int eb = routing_expert_blocks(E);
-    if (eb <= 4) return kNarrowKernel;
+    if (eb <= 4) return lw && T >= kResidentMinTokens && resident_npv(H, eb) > 0 ? kResidentKernel : kNarrowKernel;
     const bool rows_ok = lw && (H / 32) % row_stage_ksteps(eb) == 0;
     if (!rows_ok) return kWideKernel;
     return T <= kQuartersMaxTokens ? kQuartersKernel : kRowsKernel;
@@ -1055,6 +1371,7 @@ int routing_tokens_per_block(int T, int H, int E, bool lw) {
     switch (routing_kernel(T, H, E, lw)) {
         case kRowsKernel: return kRowTokens;
         case kQuartersKernel: return 16;
+        case kResidentKernel: return 16 * res_blocks_per_wg(T);
         case kWideKernel: return kWideTokens;
         default: return kTokensPerBlock * narrow_token_blocks(T, eb);
     }
@@ -1064,6 +1381,7 @@ int routing_block_threads(int T, int H, int E, bool lw) {
     switch (routing_kernel(T, H, E, lw)) {
         case kRowsKernel: return kRowWaves * kWave;
         case kQuartersKernel: return 4 * kWave;
+        case kResidentKernel: return kResWaves * kWave;
         case kWideKernel: return kWideWaves * kWave;
         default: return waves_for(eb, narrow_token_blocks(T, eb)) * kWave;
     }
@@ -1073,6 +1391,7 @@ int routing_lds_bytes(int T, int H, int E, bool lw) {
     switch (routing_kernel(T, H, E, lw)) {
         case kRowsKernel: return static_cast<int>(row_lds_bytes(eb));
         case kQuartersKernel: return static_cast<int>(quarter_lds_bytes(eb));
+        case kResidentKernel: return static_cast<int>(res_lds_bytes(eb));
         case kWideKernel: return static_cast<int>(wide_lds_bytes(eb));
         default: return static_cast<int>(narrow_lds_bytes(eb, narrow_token_blocks(T, eb), lw));
     }
@@ -1092,6 +1411,8 @@ hipError_t launch_routing_topk(const uint16_t* x, const uint16_t* w_gate, int32_
         case kQuartersKernel:
             return eb == 8 ? launch_quarters<8>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream)
                            : launch_quarters<16>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);
+        case kResidentKernel:
+            return launch_resident_eb<4>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);
         default: break;
     }
     switch (eb) {

@@ -103,9 +103,21 @@ def test_plans(lib):
     assert lib.moe_routing_topk_plan(2048, 2048, 64, 6, C.byref(rp)) == MOE_OK
     # 4 waves x (16 tokens x 64 experts of fp32 partials + a w_gate stage of 32 rows x 64 fp16 experts)
     assert (rp.grid, rp.block, rp.tokens_per_block, rp.lds_bytes) == (128, 256, 16, 4 * (16 * 64 * 4 + 32 * 64 * 2))
+    # 32 < E <= 64 below 32768 tokens: the narrow kernel, at most 2 token blocks a workgroup, so two 48 KB
+    # workgroups share a CU
     assert lib.moe_routing_topk_plan(16384, 2048, 64, 6, C.byref(rp)) == MOE_OK
-    # at most 2 token blocks for 32 < E <= 64, so two 48 KB workgroups share a CU
     assert (rp.grid, rp.block, rp.tokens_per_block, rp.lds_bytes) == (512, 256, 32, 4 * (32 * 64 * 4 + 32 * 64 * 2))
+    # from 32768 tokens (H a multiple of 1024): the resident kernel, one 8-wave workgroup per CU over a run of
+    # 16-token blocks (8 at T = 32768), an x ring of four 32 KB slots, the partials of 4 virtual waves and the
+    # logits of 4 blocks awaiting selection
+    assert lib.moe_routing_topk_plan(32768, 2048, 64, 6, C.byref(rp)) == MOE_OK
+    assert (rp.grid, rp.block, rp.tokens_per_block) == (256, 512, 128)
+    assert rp.lds_bytes == 4 * 32768 + 4 * 16 * 64 * 4 + 4 * 16 * 64 * 4 == 160 * 1024
+    assert lib.moe_routing_topk_plan(32780, 2048, 64, 6, C.byref(rp)) == MOE_OK  # 2049 blocks: 9 a workgroup
+    assert (rp.grid, rp.block, rp.tokens_per_block) == (228, 512, 144)
+    assert lib.moe_routing_topk_plan(32768, 1536, 64, 6, C.byref(rp)) == MOE_OK  # H not a multiple of 1024
+    assert (rp.grid, rp.block, rp.tokens_per_block) == (1024, 256, 32)
+    # E <= 32: the narrow kernel at any T (16 waves, up to 4 token blocks a workgroup)
     assert lib.moe_routing_topk_plan(8192, 2048, 16, 2, C.byref(rp)) == MOE_OK
     assert (rp.grid, rp.block, rp.tokens_per_block, rp.lds_bytes) == (256, 1024, 32, 16 * (32 * 16 * 4 + 32 * 16 * 2))
     # E > 64: 64 tokens per workgroup; the rows kernel (4 waves of 16 tokens over all of H, four 16 KB w_gate

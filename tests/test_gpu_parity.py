@@ -319,6 +319,32 @@ def test_routing_is_batch_invariant(ops, E, K):
     assert np.array_equal(host(w_all)[:1000].view(np.uint16), host(w_few).view(np.uint16))
 
 
+@pytest.mark.parametrize("T,H,E,K", [
+    (32790, 2048, 64, 6),  # DeepSeek-V2-Lite's routing, T ragged: runs of 9 token blocks, 8 pairs a virtual wave,
+                           # selection rounds of 4, 4 and 1 blocks
+    (33000, 1024, 48, 5),  # one ring slot a token block, the last expert block padding
+    (40000, 2048, 40, 4),  # runs of 10 blocks (250 workgroups), 24 padded experts
+    (65536, 1024, 64, 8),  # 4 pairs a virtual wave, 16 blocks a run
+])
+def test_routing_resident_kernel_matches_narrow(ops, T, H, E, K):
+    """32 < E <= 64 from 32768 tokens (H a multiple of 1024): the resident kernel holds w_gate in registers and
+    streams x through an LDS ring. It keeps the narrow kernel's summation order, so its ids and weights equal, bit
+    for bit, those of the narrow kernel for the same tokens routed in a smaller batch (the first 1000, and the last
+    600, which end in a partial token block), and every token is checked against the oracle."""
+    log(f"[resident] T={T} H={H} E={E} K={K}")
+    rng = np.random.default_rng(T + H + E)
+    x = rng.standard_normal((T, H)).astype(np.float16)
+    wg = (rng.standard_normal((H, E)) / math.sqrt(H)).astype(np.float16)
+    x_d, wg_d = dev(x), dev(wg)
+    ids_all, w_all = ops.MoeRoutingTopK(x_d, wg_d, K)
+    ids_all, w_all = host(ids_all), host(w_all)
+    for lo, hi in ((0, 1000), (T - 600, T)):
+        ids_few, w_few = ops.MoeRoutingTopK(x_d[lo:hi].contiguous(), wg_d, K)
+        assert np.array_equal(ids_all[lo:hi], host(ids_few)), (lo, hi)
+        assert np.array_equal(w_all[lo:hi].view(np.uint16), host(w_few).view(np.uint16)), (lo, hi)
+    check_routing(ids_all, w_all, x, wg, K, f"resident T{T} H{H} E{E} K{K}")
+
+
 @pytest.mark.parametrize("H,E,K", [
     (7168, 256, 8),  # DeepSeek-V3's routing: 224 stages, 56 a quarter
     (2048, 128, 6),  # two k-steps a stage (E = 128): 32 stages
