@@ -1182,6 +1182,8 @@ def test_concurrent_threads_and_streams(ops):
     (1000, 128, 100, 64, 128, 1),  # wide kernel, K = 64: 4096 slots per block, two passes
     (4096, 256, 128, 8, 128, 1),   # E = 128, T <= 8192: the quarters kernel ranks its 16-token blocks
     (9000, 256, 128, 4, 128, 1),   # E = 128, T > 8192: the rows kernel ranks its 64-token blocks
+    (32790, 1024, 64, 6, 128, 1),  # 32 < E <= 64, T >= 32768: the resident kernel ranks each workgroup's run of
+                                   # 9 token blocks (144 tokens, 864 slots) in one pass
 ])
 def test_fused_layer_matches_oracle_and_operators(ops, T, H, E, K, I, schedule):
     """moe_layer (routing that also ranks its blocks' slots, one scatter launch, the FFN, the combine): ids and
