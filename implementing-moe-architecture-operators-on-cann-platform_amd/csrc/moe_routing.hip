@@ -20,7 +20,7 @@
 //            renormalisation with all-reduces over the token's lanes (select_row): max,
 //            expf(l - max), sum, division by the sum; K rounds of an arg-max (lowest index wins an exact tie); the
 //            renormalising sum over the K picks in rank order; fp16 round-to-nearest-even.
-// From 32768 tokens, for 32 < E <= 64 (H a multiple of 1024), the resident kernel replaces the narrow one with the
+// From 32768 tokens, for 32 < E <= 64 and H = 1024 or 2048, the resident kernel replaces the narrow one with the
 // same bits: one workgroup per CU holds the narrow kernel's w_gate fragments in registers and streams x through
 // an LDS ring, so w_gate is read once per CU instead of once per 32 tokens.
 // For E > 64 the rows kernel runs above 8192 tokens: a workgroup owns 64 tokens and each of its 4 waves 16 of them
@@ -927,15 +927,15 @@ __global__ __launch_bounds__(4 * kWave) void routing_quarters_kernel(const uint1
     }
 }
 
-// ---- resident kernel: E <= 64 at large T, w_gate held in registers ----
+// ---- resident kernel: 32 < E <= 64 at large T, w_gate held in registers ----
 // The narrow kernel's workgroups each route 16-64 tokens and multiply all of w_gate into them, so at T = 16384,
 // E = 64 they read 128 MB of w_gate from L2 beside 64 MB of x, four dependent round trips a wave. This kernel is
 // persistent (one workgroup per CU, a contiguous run of 16-token blocks each) and reads w_gate once per
 // workgroup: its 8 waves hold every B fragment of the narrow kernel in VGPRs. x streams through an LDS ring of
 // 32 KB slots (16 token rows x 1024 columns), copied straight from memory into LDS a few slots ahead.
-// Same bits as the narrow kernel: the narrow kernel's W waves are kept as virtual waves v (wave v's k-step pairs
-// v, v + W, ..., each pair's two k-steps in order, on the same MFMA chain), each physical wave runs VPW virtual
-// waves for BPW of the EB expert blocks, and the W partials are folded in virtual-wave order before the same
+// Same bits as the narrow kernel: its 4 waves are kept as virtual waves v (wave v's k-step pairs v, v + 4, ...,
+// each pair's two k-steps in order, on the same MFMA chain), physical wave w runs virtual wave w / 2 for expert
+// blocks 2 (w % 2) and 2 (w % 2) + 1, and the 4 partials are folded in virtual-wave order before the same
 // selection. Fragments are read from the narrow kernel's w_gate stage layout (wstage_chunk, ds_read_b64_tr_b16).
 // LDS of a ring slot: token row r at r * 2048 bytes; 16-byte granule g of the row at g ^ r, so the 16 rows an
 // A-fragment read touches lie in distinct banks.
@@ -943,18 +943,12 @@ constexpr int kResWaves = 8;
 constexpr int kResChunk = 1024;                                  // x columns per ring slot (32 k-steps)
 constexpr int kResSlotBytes = 16 * kResChunk * 2;                // 32 KB
 constexpr int kResCopies = kResSlotBytes / 1024 / kResWaves;     // 1 KB copies per wave and slot: 4
-constexpr int res_slots(int eb) { return eb == 2 ? 3 : 4; }      // with the partials, within 160 KB of LDS
-constexpr int res_vw(int eb) { return waves_for(eb, 1); }       // the narrow kernel's waves
-constexpr int res_vpw(int eb) { return res_vw(eb) >= kResWaves ? res_vw(eb) / kResWaves : 1; }
-constexpr int res_bpw(int eb) { return eb * res_vw(eb) / kResWaves / res_vpw(eb); }
-// B fragments a wave holds for NPV pairs per virtual wave (H = 64 W NPV): at most 32 (128 VGPRs)
-constexpr int res_frags(int eb, int npv) { return res_vpw(eb) * res_bpw(eb) * npv * 2; }
-// Token blocks whose folded logits wait in LDS for one selection round of all 8 waves (16 KB of them)
-constexpr int res_sel_blocks(int eb) { return 16 / eb; }
-constexpr size_t res_lds_bytes(int eb) {
-    return static_cast<size_t>(res_slots(eb)) * kResSlotBytes + static_cast<size_t>(res_vw(eb)) * 16 * eb * 16 * 4 +
-           static_cast<size_t>(res_sel_blocks(eb)) * 16 * eb * 16 * 4;
-}
+constexpr int kResEB = 4;                                        // expert blocks (32 < E <= 64)
+constexpr int kResVW = waves_for(kResEB, 1);                     // the narrow kernel's waves: 4 virtual waves
+constexpr int kResSlots = 4;                                     // ring slots
+constexpr int kResSel = 4;  // token blocks whose folded logits wait for one selection round of all 8 waves
+// ring, partials [4 virtual waves][16 tokens][64], logits [4 blocks][16 tokens][64]: 160 KB
+constexpr size_t kResLdsBytes = static_cast<size_t>(kResSlots) * kResSlotBytes + (kResVW + kResSel) * 16 * 64 * 4;
 // Workgroups of the persistent grid: one per CU of the MI355X.
 constexpr int kResGrid = 256;
 int res_blocks_per_wg(int T) {
@@ -988,7 +982,8 @@ __device__ __forceinline__ void lds_read_tr16_x4(const uint8_t* p0, const uint8_
         : "v"(lds_addr(p0)), "v"(lds_addr(p1)), "v"(lds_addr(p2)), "v"(lds_addr(p3)));
 }
 
-template <int EB, int NPV, bool NTX>
+// NPV: k-step pairs per virtual wave (H = 256 NPV); a wave holds 4 NPV B fragments, 128 VGPRs at NPV = 8.
+template <int NPV, bool NTX>
 __global__ __launch_bounds__(kResWaves * kWave) void routing_resident_kernel(const uint16_t* __restrict__ x,
                                                                              const uint16_t* __restrict__ w_gate,
                                                                              int32_t* __restrict__ expert_ids,
@@ -996,23 +991,21 @@ __global__ __launch_bounds__(kResWaves * kWave) void routing_resident_kernel(con
                                                                              int H, int E, int K, int bpw,
                                                                              int32_t* __restrict__ counts,
                                                                              int32_t* __restrict__ rank) {
-    constexpr int VW = res_vw(EB), VPW = res_vpw(EB), BPW = res_bpw(EB);
+    constexpr int EB = kResEB, VW = kResVW, R = kResSlots, SB = kResSel;
+    constexpr int VPW = 1, BPW = 2;  // virtual waves and expert blocks of a physical wave
     constexpr int Epad = EB * 16;
-    constexpr int R = res_slots(EB);
     constexpr int PPC = 16 / VW;      // pairs of a virtual wave in one slot (32 k-steps = 16 pairs)
     constexpr int NCH = NPV / PPC;    // slots per token block: H / kResChunk
-    static_assert(NCH * PPC == NPV && res_frags(EB, NPV) <= 32, "resident geometry");
-    static_assert(BPW == 2, "the fragment reads take two expert blocks at a time");
+    static_assert(NCH * PPC == NPV && VPW * BPW * kResWaves == VW * EB, "resident geometry");
     extern __shared__ __align__(16) uint8_t lds[];
-    constexpr int SB = res_sel_blocks(EB);
     float* part = reinterpret_cast<float*>(lds + R * kResSlotBytes);  // [VW][16 tokens][Epad]
     float* logit = part + VW * 16 * Epad;                              // [SB][16 tokens][Epad]
     const int lane = lane_id();
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
     const int row = lane & 15, kg = lane >> 4;
-    // this wave's virtual waves v0 .. v0 + VPW - 1 and expert blocks b0 .. b0 + BPW - 1
-    const int v0 = VW >= kResWaves ? wave * VPW : wave / (kResWaves / VW);
-    const int b0 = VW >= kResWaves ? 0 : (wave % (kResWaves / VW)) * BPW;
+    // this wave's virtual wave v0 and expert blocks b0, b0 + 1
+    const int v0 = wave / (kResWaves / VW);
+    const int b0 = (wave % (kResWaves / VW)) * BPW;
     const int nblocks = (T + 15) / 16;
     const int blk0 = static_cast<int>(blockIdx.x) * bpw;  // the host sizes the grid so that blk0 < nblocks
     const int blk1 = min(nblocks, blk0 + bpw);
@@ -1043,7 +1036,7 @@ __global__ __launch_bounds__(kResWaves * kWave) void routing_resident_kernel(con
     f16x8 wf[VPW][BPW][NPV][2];
     {
         constexpr int kStep = EB * 1024;  // one k-step's 32 rows x Epad, 2 Epad 16-byte chunks a row
-        constexpr int kStaging = static_cast<int>(res_lds_bytes(EB)) - (R - 1) * kResSlotBytes;
+        constexpr int kStaging = static_cast<int>(kResLdsBytes) - (R - 1) * kResSlotBytes;
         uint8_t* stage0 = lds + (R - 1) * kResSlotBytes;
         const int kpp = kStaging / kStep;
         const int nsteps = H / 32;
@@ -1242,60 +1235,31 @@ hipError_t launch_eb(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, ui
     }
 }
 
-template <int EB, int NPV, bool NTX>
+template <int NPV, bool NTX>
 hipError_t launch_resident_nt(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H,
                               int E, int K, int32_t* counts, int32_t* rank, hipStream_t stream) {
     const int bpw = res_blocks_per_wg(T);
     const int grid = ((T + 15) / 16 + bpw - 1) / bpw;
-    const size_t lds = res_lds_bytes(EB);
-    const hipError_t attr = ensure_lds_limit(reinterpret_cast<const void*>(&routing_resident_kernel<EB, NPV, NTX>),
-                                             static_cast<int>(lds));
+    const hipError_t attr = ensure_lds_limit(reinterpret_cast<const void*>(&routing_resident_kernel<NPV, NTX>),
+                                             static_cast<int>(kResLdsBytes));
     if (attr != hipSuccess) return attr;
     TraceScope trace("moe_routing_topk", stream);
-    routing_resident_kernel<EB, NPV, NTX><<<grid, kResWaves * kWave, lds, stream>>>(x, w_gate, ids, w, T, H, E, K, bpw,
-                                                                                     counts, rank);
+    routing_resident_kernel<NPV, NTX><<<grid, kResWaves * kWave, kResLdsBytes, stream>>>(x, w_gate, ids, w, T, H, E, K,
+                                                                                         bpw, counts, rank);
     return hipGetLastError();
 }
 
-template <int EB, int NPV>
+template <int NPV>
 hipError_t launch_resident(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H, int E,
                            int K, int32_t* counts, int32_t* rank, hipStream_t stream) {
     if (static_cast<int64_t>(T) * H * 2 >= kNtXBytes)
-        return launch_resident_nt<EB, NPV, true>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);
-    return launch_resident_nt<EB, NPV, false>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);
+        return launch_resident_nt<NPV, true>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);
+    return launch_resident_nt<NPV, false>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);
 }
 
-// pairs per virtual wave of the resident kernel for this shape, or 0 where it does not run (H a multiple of
-// 1024 and of 64 W, the fragments within 128 VGPRs, an instantiated NPV)
-int resident_npv(int H, int eb) {
-    if (eb != 4 || H % kResChunk != 0) return 0;
-    const int vw = res_vw(eb);
-    if (H % (64 * vw) != 0) return 0;
-    const int npv = H / (64 * vw);
-    if (npv != 2 && npv != 4 && npv != 8) return 0;
-    return res_frags(eb, npv) <= 32 ? npv : 0;
-}
-
-template <int EB>
-hipError_t launch_resident_eb(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H,
-                              int E, int K, int32_t* counts, int32_t* rank, hipStream_t stream) {
-    switch (resident_npv(H, EB)) {
-        case 2:
-            if constexpr (res_frags(EB, 2) <= 32 && (2 * res_vw(EB)) % 16 == 0)
-                return launch_resident<EB, 2>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);
-            break;
-        case 4:
-            if constexpr (res_frags(EB, 4) <= 32 && (4 * res_vw(EB)) % 16 == 0)
-                return launch_resident<EB, 4>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);
-            break;
-        case 8:
-            if constexpr (res_frags(EB, 8) <= 32 && (8 * res_vw(EB)) % 16 == 0)
-                return launch_resident<EB, 8>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);
-            break;
-        default: break;
-    }
-    return hipErrorInvalidValue;
-}
+// The resident kernel's shapes: 32 < E <= 64 (four expert blocks) and H = 1024 or 2048 (4 or 8 k-step pairs per
+// virtual wave; whole 1024-column ring slots, the fragments within 128 VGPRs).
+bool resident_shape(int H, int eb) { return eb == kResEB && (H == 1024 || H == 2048); }
 
 template <int EB>
 hipError_t launch_quarters(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H, int E,
@@ -1347,7 +1311,7 @@ constexpr int64_t kQuartersMaxTokens = 8192;
 constexpr int64_t kResidentMinTokens = 32768;
 RoutingKernel routing_kernel(int T, int H, int E, bool lw) {
     const int eb = routing_expert_blocks(E);
-    if (eb <= 4) return lw && T >= kResidentMinTokens && resident_npv(H, eb) > 0 ? kResidentKernel : kNarrowKernel;
+    if (eb <= 4) return lw && T >= kResidentMinTokens && resident_shape(H, eb) ? kResidentKernel : kNarrowKernel;
     const bool rows_ok = lw && (H / 32) % row_stage_ksteps(eb) == 0;
     if (!rows_ok) return kWideKernel;
     return T <= kQuartersMaxTokens ? kQuartersKernel : kRowsKernel;
@@ -1391,7 +1355,7 @@ int routing_lds_bytes(int T, int H, int E, bool lw) {
     switch (routing_kernel(T, H, E, lw)) {
         case kRowsKernel: return static_cast<int>(row_lds_bytes(eb));
         case kQuartersKernel: return static_cast<int>(quarter_lds_bytes(eb));
-        case kResidentKernel: return static_cast<int>(res_lds_bytes(eb));
+        case kResidentKernel: return static_cast<int>(kResLdsBytes);
         case kWideKernel: return static_cast<int>(wide_lds_bytes(eb));
         default: return static_cast<int>(narrow_lds_bytes(eb, narrow_token_blocks(T, eb), lw));
     }
@@ -1412,7 +1376,8 @@ hipError_t launch_routing_topk(const uint16_t* x, const uint16_t* w_gate, int32_
             return eb == 8 ? launch_quarters<8>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream)
                            : launch_quarters<16>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);
         case kResidentKernel:
-            return launch_resident_eb<4>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);
+            return H == 1024 ? launch_resident<4>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream)
+                             : launch_resident<8>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);
         default: break;
     }
     switch (eb) {

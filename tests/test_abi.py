@@ -107,7 +107,7 @@ def test_plans(lib):
     # workgroups share a CU
     assert lib.moe_routing_topk_plan(16384, 2048, 64, 6, C.byref(rp)) == MOE_OK
     assert (rp.grid, rp.block, rp.tokens_per_block, rp.lds_bytes) == (512, 256, 32, 4 * (32 * 64 * 4 + 32 * 64 * 2))
-    # from 32768 tokens (H a multiple of 1024): the resident kernel, one 8-wave workgroup per CU over a run of
+    # from 32768 tokens (H = 1024 or 2048): the resident kernel, one 8-wave workgroup per CU over a run of
     # 16-token blocks (8 at T = 32768), an x ring of four 32 KB slots, the partials of 4 virtual waves and the
     # logits of 4 blocks awaiting selection
     assert lib.moe_routing_topk_plan(32768, 2048, 64, 6, C.byref(rp)) == MOE_OK
@@ -115,7 +115,7 @@ def test_plans(lib):
     assert rp.lds_bytes == 4 * 32768 + 4 * 16 * 64 * 4 + 4 * 16 * 64 * 4 == 160 * 1024
     assert lib.moe_routing_topk_plan(32780, 2048, 64, 6, C.byref(rp)) == MOE_OK  # 2049 blocks: 9 a workgroup
     assert (rp.grid, rp.block, rp.tokens_per_block) == (228, 512, 144)
-    assert lib.moe_routing_topk_plan(32768, 1536, 64, 6, C.byref(rp)) == MOE_OK  # H not a multiple of 1024
+    assert lib.moe_routing_topk_plan(32768, 4096, 64, 6, C.byref(rp)) == MOE_OK  # H not 1024 or 2048: narrow
     assert (rp.grid, rp.block, rp.tokens_per_block) == (1024, 256, 32)
     # E <= 32: the narrow kernel at any T (16 waves, up to 4 token blocks a workgroup)
     assert lib.moe_routing_topk_plan(8192, 2048, 16, 2, C.byref(rp)) == MOE_OK

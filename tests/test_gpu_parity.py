@@ -327,7 +327,7 @@ def test_routing_is_batch_invariant(ops, E, K):
     (65536, 1024, 64, 8),  # 4 pairs a virtual wave, 16 blocks a run
 ])
 def test_routing_resident_kernel_matches_narrow(ops, T, H, E, K):
-    """32 < E <= 64 from 32768 tokens (H a multiple of 1024): the resident kernel holds w_gate in registers and
+    """32 < E <= 64 from 32768 tokens (H = 1024 or 2048): the resident kernel holds w_gate in registers and
     streams x through an LDS ring. It keeps the narrow kernel's summation order, so its ids and weights equal, bit
     for bit, those of the narrow kernel for the same tokens routed in a smaller batch (the first 1000, and the last
     600, which end in a partial token block), and every token is checked against the oracle."""
