@@ -39,6 +39,12 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 constexpr int64_t kMaxExperts = 256;
 constexpr int64_t kInt32Max = 2147483647;
+// hiddenSize and intermediateSize bound: far above any model's, and small enough that the products of sizes the
+// checks below form stay within 64 bits
+constexpr int64_t kMaxDim = int64_t{1} << 20;
+
+// a * b > limit for a, b >= 0, without forming a product that could overflow
+bool product_exceeds(int64_t a, int64_t b, int64_t limit) { return b != 0 && a > limit / b; }
 
 // Scalar checks shared by the planners and launches.
 moe_status check_routing_sizes(int64_t T, int64_t H, int64_t E, int64_t K) {
@@ -47,7 +53,8 @@ moe_status check_routing_sizes(int64_t T, int64_t H, int64_t E, int64_t K) {
     if (K < 1 || K > E) return fail(MOE_ERR_ARG, "topK=%lld must be in [1, numExperts=%lld]", (long long)K, (long long)E);
     if (H % 32 != 0) return fail(MOE_ERR_UNSUPPORTED, "hiddenSize=%lld must be a multiple of 32", (long long)H);
     if (E > kMaxExperts) return fail(MOE_ERR_UNSUPPORTED, "numExperts=%lld exceeds %lld", (long long)E, (long long)kMaxExperts);
-    if (T * H > kInt32Max * 8LL || T * K > kInt32Max)
+    if (H > kMaxDim) return fail(MOE_ERR_UNSUPPORTED, "hiddenSize=%lld exceeds %lld", (long long)H, (long long)kMaxDim);
+    if (product_exceeds(T, H, kInt32Max * 8LL) || product_exceeds(T, K, kInt32Max))
         return fail(MOE_ERR_UNSUPPORTED, "T=%lld too large", (long long)T);
     return ok();
 }
@@ -57,6 +64,8 @@ moe_status check_ffn_sizes(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I
     if (st != MOE_OK) return st;
     if (I <= 0) return fail(MOE_ERR_ARG, "intermediateSize=%lld must be > 0", (long long)I);
     if (I % 32 != 0) return fail(MOE_ERR_UNSUPPORTED, "intermediateSize=%lld must be a multiple of 32", (long long)I);
+    if (I > kMaxDim)
+        return fail(MOE_ERR_UNSUPPORTED, "intermediateSize=%lld exceeds %lld", (long long)I, (long long)kMaxDim);
     if (moe::ffn_schedule(T, H, E, K, I) < 0) {
         if (moe::tiled_shape_supported(H, E, I) && !moe::tiled_size_supported(T, H, K, I))
             return fail(MOE_ERR_UNSUPPORTED,
@@ -66,7 +75,7 @@ moe_status check_ffn_sizes(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I
         return fail(MOE_ERR_UNSUPPORTED, "hiddenSize=%lld / intermediateSize=%lld: no expert GEMM schedule fits",
                     (long long)H, (long long)I);
     }
-    if (T * K * I > kInt32Max * 64LL) return fail(MOE_ERR_UNSUPPORTED, "T*K*I too large");
+    if (product_exceeds(T * K, I, kInt32Max * 64LL)) return fail(MOE_ERR_UNSUPPORTED, "T*K*I too large");  // T*K <= 2^31
     return ok();
 }
 
@@ -75,7 +84,8 @@ moe_status check_combine_sizes(int64_t T, int64_t H, int64_t K) {
         return fail(MOE_ERR_ARG, "sizes must be T >= 0, H > 0, K >= 1 (T=%lld H=%lld K=%lld)", (long long)T,
                     (long long)H, (long long)K);
     if (H % 8 != 0) return fail(MOE_ERR_UNSUPPORTED, "hiddenSize=%lld must be a multiple of 8", (long long)H);
-    if (T * K > kInt32Max) return fail(MOE_ERR_UNSUPPORTED, "T*K too large");
+    if (H > kMaxDim) return fail(MOE_ERR_UNSUPPORTED, "hiddenSize=%lld exceeds %lld", (long long)H, (long long)kMaxDim);
+    if (product_exceeds(T, K, kInt32Max)) return fail(MOE_ERR_UNSUPPORTED, "T*K too large");
     return ok();
 }
 

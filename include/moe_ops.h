@@ -26,8 +26,8 @@
  * The reference's NPU kernel reads W_down as [I, H] (op_kernel/moe_expert_ffn.cpp:348-375); both of its CPU
  * references use [H, I], and this library follows the CPU references.
  *
- * Limits of the gfx950 kernels (MOE_ERR_UNSUPPORTED otherwise): H % 32 == 0, I % 32 == 0,
- * 1 <= K <= E <= 256, T*K < 2^31, and 16-byte aligned x, expert_weights, expert_out and y.
+ * Limits of the gfx950 kernels (MOE_ERR_UNSUPPORTED otherwise): H % 32 == 0, I % 32 == 0, H and I at most
+ * 2^20, 1 <= K <= E <= 256, T*K < 2^31, and 16-byte aligned x, expert_weights, expert_out and y.
  * Calls with many rows per expert (the LDS-tiled schedule, moe_expert_ffn_plan .schedule == 1) also need
  * T*H*2 (x), 3*I*H*2 (one expert's weights) and T*K*4 (the sorted slots) below 2 GiB: the tiled kernels address
  * them with 32-bit buffer offsets. Such calls beyond those bounds are rejected with the reason rather than run
