@@ -70,8 +70,8 @@ constexpr int kMaxParts = 256;
 constexpr int kFixThreads = 256;
 constexpr int kFixRows = 16;  // tile rows per fix-up workgroup
 // The split pays off only while the leftover round is a large share of the down projection: at DeepSeek-V2-Lite
-// prefill (T = 16384, E = 64, K = 6, 13-14 rounds of 22-stage tiles) the unsplit kernel takes 651 us against
-// 677 us + a 17 us fix-up split; at 2-2.5 rounds (T = 8192, E = 16; Mixtral T = 4096) the split saves 100-215 us.
+// prefill (T = 16384, E = 64, K = 6, 13-14 rounds of 22-stage tiles) the unsplit kernel takes 575 us against
+// 589 us + a 15 us fix-up split; at 2-2.5 rounds (T = 8192, E = 16; Mixtral T = 4096) the split saves 100-215 us.
 constexpr int kSplitMaxRounds = 4;
 
 struct TiledArgs {
