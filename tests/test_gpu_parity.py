@@ -449,6 +449,37 @@ def test_ffn_edge_routings(ops):
     within(oracle.compare(eo[mask], eo_o[mask]), max_abs=1e-2, mean_abs=1e-3, cos=0.9999)
 
 
+@pytest.mark.parametrize("T,H,E,K,I,schedule", [
+    (50, 128, 8, 3, 128, 0),     # 32-row weight streaming
+    (300, 256, 16, 2, 256, 0),   # wide weight streaming (~34 valid rows per expert)
+    (3000, 128, 8, 3, 128, 1),   # tiled, several m-tiles per expert
+    (700, 256, 32, 4, 192, 1),   # tiled, I = 6 x 32 (odd multiple of 32 on the down reduction)
+])
+def test_ffn_arbitrary_caller_ids(ops, T, H, E, K, I, schedule):
+    """MoeExpertFFN takes expert_ids from its caller, not only from the routing operator: uniformly random ids in
+    [-2, E + 2) put one token on the same expert twice, leave some slots without an expert and skew the experts'
+    row counts. On every FFN schedule: offsets and sorted_slot equal a stable sort of the valid slots, the slots of
+    ids outside [0, E) are zero rows, and every other slot matches the oracle FFN (tests/moe_cpu_sim.cpp:245-296)."""
+    assert ffn_schedule(T, H, E, K, I) == schedule
+    rng = np.random.default_rng(T * 7 + E)
+    x = rng.standard_normal((T, H)).astype(np.float16)
+    ew = np.concatenate([rng.standard_normal((E, 2 * I, H)) / math.sqrt(H),
+                         rng.standard_normal((E, I, H)) / math.sqrt(I)], axis=1).astype(np.float16)
+    ids = rng.integers(-2, E + 2, size=(T, K)).astype(np.int32)
+    valid = (ids >= 0) & (ids < E)
+    dup = int(sum(len(r) - len(set(r)) for r in np.where(valid, ids, -1 - np.arange(K)).tolist()))
+    log(f"[caller ids] T={T} H={H} E={E} K={K} I={I} schedule={schedule}: {int((~valid).sum())} invalid slots, "
+        f"{dup} repeated experts within a token")
+    assert dup > 0 and (~valid).any()
+    w = np.full((T, K), 0.25, np.float16)
+    eo_d, ws = run_ffn(ops, dev(x), dev(ids), dev(w), dev(ew), I)
+    eo = f32(host(eo_d))
+    check_permute(host(ws), ids, E)
+    assert not eo[~valid].any()
+    eo_o = oracle_ffn_threads(f32(x), np.where(valid, ids, 0).astype(np.int32), f32(ew), I)
+    within(oracle.compare(eo[valid], eo_o[valid]), max_abs=1e-2, mean_abs=1e-3, cos=0.9999)
+
+
 @pytest.mark.parametrize("T,H,E,K,I,pattern", [
     (100, 64, 8, 2, 96, "skewed"),      # one expert 150 rows (5 passes of 32), one the rest, six empty
     (1000, 64, 16, 1, 64, "uniform"),   # S = 1000: each wave's id scan runs several unrolled rounds
