@@ -983,7 +983,8 @@ __device__ __forceinline__ void lds_read_tr16_x4(const uint8_t* p0, const uint8_
 }
 
 // NPV: k-step pairs per virtual wave (H = 256 NPV); a wave holds 4 NPV B fragments, 128 VGPRs at NPV = 8.
-template <int NPV, bool NTX>
+// x is loaded non-temporally: from 32768 tokens at H >= 1024 it is at least 64 MB (kNtXBytes).
+template <int NPV>
 __global__ __launch_bounds__(kResWaves * kWave) void routing_resident_kernel(const uint16_t* __restrict__ x,
                                                                              const uint16_t* __restrict__ w_gate,
                                                                              int32_t* __restrict__ expert_ids,
@@ -1027,7 +1028,7 @@ __global__ __launch_bounds__(kResWaves * kWave) void routing_resident_kernel(con
 #pragma unroll
         for (int m = 0; m < kResCopies; ++m)  // rows past T read zeros; their results are dropped
             __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (__attribute__((address_space(3))) void*)(dst + m * 1024), 16,
-                                                     xoff[m], c * kResChunk * 2, 0, NTX ? 2 : 0);
+                                                     xoff[m], c * kResChunk * 2, 0, 2 /* nt */);
     };
     const int nx0 = min(R - 1, nq);  // ring slots issued during the w_gate staging
 
@@ -1235,26 +1236,18 @@ hipError_t launch_eb(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, ui
     }
 }
 
-template <int NPV, bool NTX>
-hipError_t launch_resident_nt(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H,
-                              int E, int K, int32_t* counts, int32_t* rank, hipStream_t stream) {
-    const int bpw = res_blocks_per_wg(T);
-    const int grid = ((T + 15) / 16 + bpw - 1) / bpw;
-    const hipError_t attr = ensure_lds_limit(reinterpret_cast<const void*>(&routing_resident_kernel<NPV, NTX>),
-                                             static_cast<int>(kResLdsBytes));
-    if (attr != hipSuccess) return attr;
-    TraceScope trace("moe_routing_topk", stream);
-    routing_resident_kernel<NPV, NTX><<<grid, kResWaves * kWave, kResLdsBytes, stream>>>(x, w_gate, ids, w, T, H, E, K,
-                                                                                         bpw, counts, rank);
-    return hipGetLastError();
-}
-
 template <int NPV>
 hipError_t launch_resident(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H, int E,
                            int K, int32_t* counts, int32_t* rank, hipStream_t stream) {
-    if (static_cast<int64_t>(T) * H * 2 >= kNtXBytes)
-        return launch_resident_nt<NPV, true>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);
-    return launch_resident_nt<NPV, false>(x, w_gate, ids, w, T, H, E, K, counts, rank, stream);
+    const int bpw = res_blocks_per_wg(T);
+    const int grid = ((T + 15) / 16 + bpw - 1) / bpw;
+    const hipError_t attr = ensure_lds_limit(reinterpret_cast<const void*>(&routing_resident_kernel<NPV>),
+                                             static_cast<int>(kResLdsBytes));
+    if (attr != hipSuccess) return attr;
+    TraceScope trace("moe_routing_topk", stream);
+    routing_resident_kernel<NPV><<<grid, kResWaves * kWave, kResLdsBytes, stream>>>(x, w_gate, ids, w, T, H, E, K, bpw,
+                                                                                    counts, rank);
+    return hipGetLastError();
 }
 
 // The resident kernel's shapes: 32 < E <= 64 (four expert blocks) and H = 1024 or 2048 (4 or 8 k-step pairs per
@@ -1309,6 +1302,7 @@ constexpr int64_t kQuartersMaxTokens = 8192;
 // tokens at the end, where the narrow kernel's two workgroups per CU hide one's selection behind the other's
 // loads: the resident kernel gains only once a CU routes 128 tokens or more.
 constexpr int64_t kResidentMinTokens = 32768;
+static_assert(kResidentMinTokens * 1024 * 2 >= kNtXBytes, "the resident kernel always loads x non-temporally");
 RoutingKernel routing_kernel(int T, int H, int E, bool lw) {
     const int eb = routing_expert_blocks(E);
     if (eb <= 4) return lw && T >= kResidentMinTokens && resident_shape(H, eb) ? kResidentKernel : kNarrowKernel;
