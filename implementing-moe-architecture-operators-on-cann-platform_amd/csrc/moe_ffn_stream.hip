@@ -65,6 +65,18 @@ constexpr int kWaves = 8;                 // streaming waves per workgroup
 constexpr int kThreads = kWaves * kWave;  // 512
 constexpr int kMaxRows = 32;              // activation rows per pass (two 16-row MFMA tiles)
 constexpr int kWideRows = 128;            // wide kernel: activation rows per pass (eight 16-row MFMA tiles)
+// A pass over at most kWideRowsLow rows (an expert's last pass, or its only one) runs without the eight-tile path
+// and then fits a ring of kWideDepthLow k-steps in the registers. Up to kWideLowMaxRows rows per expert on average
+// the wide kernels run such passes; above it most experts need 128-row passes, and the workgroups of the experts
+// that do not finish early and leave the tail to the slower passes. The FFN at H = 2048, E = 16, K = 2, I = 8192
+// (us, 128-row passes only / with the 64-row passes): T = 256 (32 rows per expert) 330.4 / 304.9, T = 384 (48)
+// 352.6 / 325.0, T = 448 (56) 354.5 / 334.7; at T = 464 (58) an earlier build of the 64-row passes took 368.0
+// against 359.6. Mixtral's H = 4096, E = 8, I = 14336: T = 192 (48) 576.1 / 558.5, T = 224 (56) 612.0 / 598.8.
+// Running every pass of up to 64 rows that way (an expert of 65 rows in two passes) streams twice the weights of
+// every expert above 64 rows: 466.0 us at T = 464.
+constexpr int kWideRowsLow = 64;
+constexpr int kWideDepthLow = 8;
+constexpr int64_t kWideLowMaxRows = 56;
 // Ring depth of the wide kernels (k-steps in flight per wave), whatever the narrow kernels use: with 8 the wide
 // gate/up kernel spilled 33 registers in its loop and ran 8-12 % slower (T = 128, H = 4096, E = 8, I = 14336:
 // 390 against 358 us; T = 512, H = 2048, E = 16, I = 8192: 281 against 251 us).
@@ -260,7 +272,7 @@ __device__ __forceinline__ void line_pass(const StreamArgs& p, const uint16_t* l
     epilogue<MT, EPI>(p, acc0, acc1, off, ne, mc, n0, split, lane);
 }
 
-// Wide passes (up to kWideRows activation rows, MT row tiles): the K-range is staged in LDS one chunk of kchunk
+// Wide passes (up to 64 or 128 activation rows, MT row tiles): the K-range is staged in LDS one chunk of kchunk
 // columns (bpc column blocks of 64) at a time. The ring runs over the sequence of blocks chunk by chunk, each chunk
 // in the rotated order (j + rotc) % bpc, and refills each slot with the block CB places later in the sequence
 // (which may lie in the next chunk). One call multiplies the blocks of chunk c into the accumulators.
@@ -526,17 +538,17 @@ __global__ __launch_bounds__(kThreads) void ffn_stream_kernel(StreamArgs p, int 
     }
 }
 
-// One wide pass of up to kWideRows rows: for each K chunk, every wave waits for the others to finish the previous
+// One wide pass of up to 128 rows (MT row tiles): for each K chunk, every wave waits for the others to finish the previous
 // chunk, the workgroup stages the chunk's activation rows, and the active waves multiply it; the epilogue follows
 // the last chunk. The ring was primed with the first CB blocks of chunk 0.
 template <int MT, int CB, int EPI>
 __device__ __forceinline__ void wide_pass(const StreamArgs& p, uint16_t* lds, uint16_t* tb, const uint16_t* const (&wr)[4],
-                                          f16x8 (&rg)[CB][4], const int* s_rows, bool active, int rows, int rotc,
-                                          int off, int ne, int mc, int n0, int split, int lane) {
+                                          f16x8 (&rg)[CB][4], const int* s_rows, bool active, int rows, int kchunk,
+                                          int rotc, int off, int ne, int mc, int n0, int split, int lane) {
     const int tid = static_cast<int>(threadIdx.x);
-    const int bpc = p.kchunk / 64, nchunk = p.kc / p.kchunk;
-    const int stride = p.kchunk + 8;
-    const int gpr = p.kchunk / 8;  // 16-byte granules per staged row
+    const int bpc = kchunk / 64, nchunk = p.kc / kchunk;
+    const int stride = kchunk + 8;
+    const int gpr = kchunk / 8;  // 16-byte granules per staged row
     const int k0 = split * p.kc;
     f32x4 acc0[MT], acc1[MT];
 #pragma unroll
@@ -555,7 +567,7 @@ __device__ __forceinline__ void wide_pass(const StreamArgs& p, uint16_t* lds, ui
                 if (q < total) {
                     const int r = q / gpr;
                     const size_t src_row = p.gather ? static_cast<size_t>(s_rows[r] / p.K) : static_cast<size_t>(off + mc + r);
-                    v[t] = *reinterpret_cast<const u32x4*>(p.act + src_row * p.kdim + k0 + c * p.kchunk + (q % gpr) * 8);
+                    v[t] = *reinterpret_cast<const u32x4*>(p.act + src_row * p.kdim + k0 + c * kchunk + (q % gpr) * 8);
                 }
             }
 #pragma unroll
@@ -570,16 +582,51 @@ __device__ __forceinline__ void wide_pass(const StreamArgs& p, uint16_t* lds, ui
     if (active) epilogue<MT, EPI>(p, acc0, acc1, off, ne, mc, n0, split, lane);
 }
 
-// The weight-streaming schedule for up to kWideRows rows per pass (experts with ~32 to a few hundred rows): the
-// same units and full-line ring as ffn_stream_kernel, but each pass covers up to 128 rows (MT = 1, 2, 4 or 8 row
-// tiles), so an expert's weights are streamed once per 128 rows instead of once per 32, and the K-range is staged
-// in chunks of p.kchunk columns to fit 128 rows in LDS.
-template <int D, int EPI>
+// A 64-row pass stages chunks of twice the columns where the K-range allows (the LDS holds 128 rows of p.kchunk).
+template <int ROWS>
+__device__ __forceinline__ int wide_kchunk(const StreamArgs& p) {
+    return ROWS <= 64 && p.kc % (2 * p.kchunk) == 0 ? 2 * p.kchunk : p.kchunk;
+}
+
+// Rotated start of wave `wave` of unit u inside each chunk, a multiple of CB (so a batch of CB blocks never wraps).
+template <int CB>
+__device__ __forceinline__ int wide_rotation(const StreamArgs& p, int u, int wave, int kchunk) {
+    return (((u * kWaves + wave) * 7 * CB) % (p.kc / 64)) % (kchunk / 64) / CB * CB;
+}
+
+// One pass of the wide kernel over up to ROWS rows of expert e from row mc, with a ring of CB k-step pairs: primes
+// the ring, ranks the pass's rows (gate/up) and multiplies them in MT-tile passes.
+template <int CB, int EPI, int ROWS>
+__device__ __forceinline__ void wide_rows(const StreamArgs& p, uint16_t* lds, uint16_t* tb, const uint16_t* const (&wr)[4],
+                                          int* s_rows, bool active, int kchunk, int rotc, int e, int before, int off,
+                                          int ne, int mc, int n0, int split, int32_t* sorted, int lane) {
+    const int rows = min(ROWS, ne - mc);
+    f16x8 rg[CB][4];
+    if (active) line_prime<CB>(wr, rotc, rg);  // the first CB blocks of chunk 0
+    if (gate_up(EPI)) {
+        lds_barrier();  // every wave is done reading s_rows
+        expert_rank(p, e, before, off, mc, ROWS, s_rows, sorted);
+    }
+    if (rows > 64) {
+        if constexpr (ROWS > 64) wide_pass<8, CB, EPI>(p, lds, tb, wr, rg, s_rows, active, rows, kchunk, rotc, off, ne, mc, n0, split, lane);
+    } else if (rows > 32) wide_pass<4, CB, EPI>(p, lds, tb, wr, rg, s_rows, active, rows, kchunk, rotc, off, ne, mc, n0, split, lane);
+    else if (rows > 16) wide_pass<2, CB, EPI>(p, lds, tb, wr, rg, s_rows, active, rows, kchunk, rotc, off, ne, mc, n0, split, lane);
+    else wide_pass<1, CB, EPI>(p, lds, tb, wr, rg, s_rows, active, rows, kchunk, rotc, off, ne, mc, n0, split, lane);
+}
+
+// The weight-streaming schedule for experts with ~32 to a few hundred rows: the same units and full-line ring as
+// ffn_stream_kernel, but each pass covers up to kWideRows = 128 rows (MT = 1, 2, 4 or 8 row tiles, a ring of
+// kWideDepth k-steps), so an expert's weights are streamed once per 128 rows instead of once per 32, and the
+// K-range is staged in chunks of p.kchunk columns to fit 128 rows in LDS. With LOW, a pass with at most
+// kWideRowsLow rows left runs as a 64-row pass with a ring of kWideDepthLow k-steps (p.kchunk a multiple of its
+// batch) and chunks of twice p.kchunk columns where the K-range divides, so an expert of up to 64 rows streams its
+// weights with twice the loads in flight and half the stages.
+template <int EPI, bool LOW>
 __global__ __launch_bounds__(kThreads) void ffn_stream_wide_kernel(StreamArgs p, int units_per_wg) {
     extern __shared__ __align__(16) uint16_t lds[];
     __shared__ int s_eq[kWaves], s_lt[kWaves];
     __shared__ int s_rows[kWideRows];
-    constexpr int CB = D / 2;
+    constexpr int CB = kWideDepth / 2, CBL = kWideDepthLow / 2;
     static_assert(CB >= 1, "the wide kernel runs the full-line ring");
     const int wave = static_cast<int>(threadIdx.x) / kWave;
     const int lane = lane_id();
@@ -589,9 +636,6 @@ __global__ __launch_bounds__(kThreads) void ffn_stream_wide_kernel(StreamArgs p,
     const int total_units = p.E * p.nsplit * groups;
     const int u_begin = static_cast<int>(blockIdx.x) * units_per_wg;
     const int u_end = min(u_begin + units_per_wg, total_units);
-    const int nblk = p.kc / 64;
-    const int bpc = p.kchunk / 64;
-
     if (gate_up(EPI)) {
         const int per = (p.S + static_cast<int>(gridDim.x) - 1) / static_cast<int>(gridDim.x);
         const int s_beg = min(p.S, static_cast<int>(blockIdx.x) * per), s_end = min(p.S, s_beg + per);
@@ -645,26 +689,42 @@ __global__ __launch_bounds__(kThreads) void ffn_stream_wide_kernel(StreamArgs p,
         const bool active = n0 < p.ndim;
         const int k0 = split * p.kc;
         const size_t ebase = static_cast<size_t>(e) * 3 * static_cast<size_t>(p.I) * p.H;
-        // rotated start inside each chunk, a multiple of CB (so a batch of CB blocks never wraps)
-        const int rotc = (((u * kWaves + wave) * 7 * CB) % nblk) % bpc / CB * CB;
         const uint16_t* wbase = p.w + ebase + p.w_off + static_cast<size_t>(active ? n0 : 0) * p.kdim + k0 +
                                 static_cast<size_t>(lane >> 3) * p.kdim + (lane & 7) * 8;
         const uint16_t* const wr[4] = {wbase, wbase + static_cast<size_t>(8) * p.kdim, wbase + p.w1_off,
                                        wbase + p.w1_off + static_cast<size_t>(8) * p.kdim};
         uint16_t* tb = lds + kWideRows * (p.kchunk + 8) + wave * 1024;
-        for (int mc = 0; mc < ne; mc += kWideRows) {
-            const int rows = min(kWideRows, ne - mc);
-            f16x8 rg[CB][4];
-            if (active) line_prime<CB>(wr, rotc, rg);  // the first CB blocks of chunk 0
-            if (gate_up(EPI)) {
-                lds_barrier();  // every wave is done reading s_rows
-                expert_rank(p, e, before, off, mc, kWideRows, s_rows,
-                            g == 0 && split == 0 && mc == 0 ? p.sorted_out : nullptr);
+        const bool rank_out = g == 0 && split == 0;  // the expert's first pass writes sorted_out
+        const int rotc = wide_rotation<CB>(p, u, wave, p.kchunk);
+        if constexpr (!LOW) {
+            // written out rather than through wide_rows: this form of the 128-row loop compiles to the faster code
+            // (about 2 % on the FFN at 64 rows per expert)
+            for (int mc = 0; mc < ne; mc += kWideRows) {
+                const int rows = min(kWideRows, ne - mc);
+                f16x8 rg[CB][4];
+                if (active) line_prime<CB>(wr, rotc, rg);  // the first CB blocks of chunk 0
+                if (gate_up(EPI)) {
+                    lds_barrier();  // every wave is done reading s_rows
+                    expert_rank(p, e, before, off, mc, kWideRows, s_rows, rank_out && mc == 0 ? p.sorted_out : nullptr);
+                }
+                if (rows > 64) wide_pass<8, CB, EPI>(p, lds, tb, wr, rg, s_rows, active, rows, p.kchunk, rotc, off, ne, mc, n0, split, lane);
+                else if (rows > 32) wide_pass<4, CB, EPI>(p, lds, tb, wr, rg, s_rows, active, rows, p.kchunk, rotc, off, ne, mc, n0, split, lane);
+                else if (rows > 16) wide_pass<2, CB, EPI>(p, lds, tb, wr, rg, s_rows, active, rows, p.kchunk, rotc, off, ne, mc, n0, split, lane);
+                else wide_pass<1, CB, EPI>(p, lds, tb, wr, rg, s_rows, active, rows, p.kchunk, rotc, off, ne, mc, n0, split, lane);
             }
-            if (rows > 64) wide_pass<8, CB, EPI>(p, lds, tb, wr, rg, s_rows, active, rows, rotc, off, ne, mc, n0, split, lane);
-            else if (rows > 32) wide_pass<4, CB, EPI>(p, lds, tb, wr, rg, s_rows, active, rows, rotc, off, ne, mc, n0, split, lane);
-            else if (rows > 16) wide_pass<2, CB, EPI>(p, lds, tb, wr, rg, s_rows, active, rows, rotc, off, ne, mc, n0, split, lane);
-            else wide_pass<1, CB, EPI>(p, lds, tb, wr, rg, s_rows, active, rows, rotc, off, ne, mc, n0, split, lane);
+        } else {
+            int32_t* const sorted = rank_out ? p.sorted_out : nullptr;
+            for (int mc = 0; mc < ne; mc += kWideRows) {  // uniform over the workgroup
+                if (ne - mc <= kWideRowsLow) {
+                    const int kch = wide_kchunk<kWideRowsLow>(p);
+                    wide_rows<CBL, EPI, kWideRowsLow>(p, lds, tb, wr, s_rows, active, kch,
+                                                      wide_rotation<CBL>(p, u, wave, kch), e, before, off, ne, mc, n0,
+                                                      split, mc == 0 ? sorted : nullptr, lane);
+                    break;  // the expert's last pass
+                }
+                wide_rows<CB, EPI, kWideRows>(p, lds, tb, wr, s_rows, active, p.kchunk, rotc, e, before, off, ne, mc,
+                                              n0, split, mc == 0 ? sorted : nullptr, lane);
+            }
         }
     }
 }
@@ -868,9 +928,9 @@ StreamShape gateup_shape(int64_t T, int H, int64_t E, int64_t K, bool allow_spli
 }
 // The wide kernels stage the K-range in chunks whatever its length, so their gate/up always takes the whole of H
 // (no partial sums); wide_chunk(H) == 0 (H not a multiple of 128) rules the wide kernels out.
-int wide_chunk(int kc);
+int wide_chunk(int kc, int rows, int depth);
 StreamShape gateup_wide_shape(int H) {
-    return wide_chunk(H) > 0 ? StreamShape{H, kWideDepth, kWideRows, 1} : StreamShape{0, 0, 0, 0};
+    return wide_chunk(H, kWideRows, kWideDepth) > 0 ? StreamShape{H, kWideDepth, kWideRows, 1} : StreamShape{0, 0, 0, 0};
 }
 
 template <int EPI>
@@ -905,24 +965,30 @@ hipError_t launch_stream_epi(const StreamArgs& p, int d, int units, hipStream_t 
 }
 
 // K columns per LDS stage of the wide kernel for a K-range kc: the largest multiple of the ring's batch
-// (64 * kWideDepth / 2 columns) dividing kc whose kWideRows rows fit the LDS beside the re-layout buffers; 0 if none.
-int wide_chunk(int kc) {
-    const int step = 64 * (kWideDepth / 2);
-    const int max_cols = (kLdsMax - kTbBytes) / (kWideRows * 2) - 8;
+// (64 * depth / 2 columns) dividing kc whose `rows` rows fit the LDS beside the re-layout buffers; 0 if none.
+int wide_chunk(int kc, int rows, int depth) {
+    const int step = 64 * (depth / 2);
+    const int max_cols = (kLdsMax - kTbBytes) / (rows * 2) - 8;
     for (int kch = max_cols / step * step; kch >= step; kch -= step)
         if (kc % kch == 0) return kch;
     return 0;
 }
 
-template <int EPI>
+template <int EPI, bool LOW>
+const void* wide_kernel_fn() {
+    return reinterpret_cast<const void*>(&ffn_stream_wide_kernel<EPI, LOW>);
+}
+
+// LOW: passes with at most kWideRowsLow rows left run the deeper ring (p.kchunk a multiple of its batch).
+template <int EPI, bool LOW>
 hipError_t launch_stream_wide(const StreamArgs& p, int units, hipStream_t stream) {
     const size_t lds = static_cast<size_t>(kWideRows) * (p.kchunk + 8) * sizeof(uint16_t) + kTbBytes;
-    const void* fn = reinterpret_cast<const void*>(&ffn_stream_wide_kernel<kWideDepth, EPI>);
+    const void* fn = wide_kernel_fn<EPI, LOW>();
     hipError_t err = ensure_lds_limit(fn, kLdsMax);
     if (err != hipSuccess) return err;
     const int slots = resident_workgroups(fn, kThreads, static_cast<int>(lds));
     const int upw = slots > 0 ? (units + slots - 1) / slots : 1;
-    ffn_stream_wide_kernel<kWideDepth, EPI><<<(units + upw - 1) / upw, kThreads, lds, stream>>>(p, upw);
+    ffn_stream_wide_kernel<EPI, LOW><<<(units + upw - 1) / upw, kThreads, lds, stream>>>(p, upw);
     return hipGetLastError();
 }
 
@@ -958,10 +1024,10 @@ hipError_t prepare_ffn_stream(int H, int I) {
         if (err != hipSuccess) return err;
     }
     if (stream_wide_supported(H, I)) {
-        const void* wide_fns[2] = {
-            reinterpret_cast<const void*>(&ffn_stream_wide_kernel<kWideDepth, kSwiGLU>),
-            dn.nsplit > 1 ? reinterpret_cast<const void*>(&ffn_stream_wide_kernel<kWideDepth, kPartial>)
-                          : reinterpret_cast<const void*>(&ffn_stream_wide_kernel<kWideDepth, kScatter>)};
+        const void* wide_fns[4] = {
+            wide_kernel_fn<kSwiGLU, false>(), wide_kernel_fn<kSwiGLU, true>(),
+            dn.nsplit > 1 ? wide_kernel_fn<kPartial, false>() : wide_kernel_fn<kScatter, false>(),
+            dn.nsplit > 1 ? wide_kernel_fn<kPartial, true>() : wide_kernel_fn<kScatter, true>()};
         for (const void* fn : wide_fns) {
             const hipError_t err = ensure_lds_limit(fn, kLdsMax);
             if (err != hipSuccess) return err;
@@ -992,7 +1058,15 @@ bool stream_supported(int H, int I, bool gateup_split) {
 // Whether the shape can run the wide kernels (both GEMMs' rings and K-ranges allow a chunked stage).
 bool stream_wide_supported(int H, int I) {
     const StreamShape gu = gateup_wide_shape(H), dn = pick_shape(I, true);
-    return gu.kc > 0 && dn.kc > 0 && wide_chunk(gu.kc) > 0 && wide_chunk(dn.kc) > 0;
+    return gu.kc > 0 && dn.kc > 0 && wide_chunk(gu.kc, kWideRows, kWideDepth) > 0 &&
+           wide_chunk(dn.kc, kWideRows, kWideDepth) > 0;
+}
+// Whether the wide kernels run their short passes with the deeper ring: up to kWideLowMaxRows rows per expert on
+// average, where both GEMMs' K-ranges allow a chunk of 128 rows that is a multiple of that ring's batch.
+bool stream_wide_low(int64_t T, int H, int64_t E, int64_t K, int I) {
+    const StreamShape gu = gateup_wide_shape(H), dn = pick_shape(I, true);
+    return T * K <= kWideLowMaxRows * E && wide_chunk(gu.kc, kWideRows, kWideDepthLow) > 0 &&
+           wide_chunk(dn.kc, kWideRows, kWideDepthLow) > 0;
 }
 
 // The wide kernels run from kWideMinRows rows per expert on average (the 32-row passes then start to repeat).
@@ -1031,6 +1105,7 @@ hipError_t launch_ffn_stream(const uint16_t* x, const int32_t* expert_ids, const
     // fp32 partial sums reduced into hidden)
     // experts with more than ~32 rows on average take the wide kernels (up to 128 rows per pass)
     const bool wide = stream_wide(T, H, E, K, I);
+    const bool low = wide && stream_wide_low(T, H, E, K, I);
     const StreamShape gu = wide ? gateup_wide_shape(H) : gateup_shape(T, H, E, K, gateup_split);
     p.act = x;
     p.out = ws.hidden;
@@ -1048,9 +1123,12 @@ hipError_t launch_ffn_stream(const uint16_t* x, const int32_t* expert_ids, const
     {
         TraceScope trace("moe_ffn_gateup_swiglu", stream);
         const int units = stream_gateup_grid(T, H, E, K, I, wide, gateup_split);
-        if (wide) {
-            p.kchunk = wide_chunk(gu.kc);
-            err = launch_stream_wide<kSwiGLU>(p, units, stream);
+        if (wide && low) {
+            p.kchunk = wide_chunk(gu.kc, kWideRows, kWideDepthLow);
+            err = launch_stream_wide<kSwiGLU, true>(p, units, stream);
+        } else if (wide) {
+            p.kchunk = wide_chunk(gu.kc, kWideRows, kWideDepth);
+            err = launch_stream_wide<kSwiGLU, false>(p, units, stream);
         } else {
             err = gu.nsplit > 1 ? launch_stream_epi<kGatePartial>(p, gu.d, units, stream)
                                 : launch_stream_epi<kSwiGLU>(p, gu.d, units, stream);
@@ -1079,10 +1157,14 @@ hipError_t launch_ffn_stream(const uint16_t* x, const int32_t* expert_ids, const
     p.gather = 0;
     {
         TraceScope trace("moe_ffn_down", stream);
-        if (wide) {
-            p.kchunk = wide_chunk(dn.kc);
-            err = dn.nsplit > 1 ? launch_stream_wide<kPartial>(p, stream_down_grid(E, H, I), stream)
-                                : launch_stream_wide<kScatter>(p, stream_down_grid(E, H, I), stream);
+        if (wide && low) {
+            p.kchunk = wide_chunk(dn.kc, kWideRows, kWideDepthLow);
+            err = dn.nsplit > 1 ? launch_stream_wide<kPartial, true>(p, stream_down_grid(E, H, I), stream)
+                                : launch_stream_wide<kScatter, true>(p, stream_down_grid(E, H, I), stream);
+        } else if (wide) {
+            p.kchunk = wide_chunk(dn.kc, kWideRows, kWideDepth);
+            err = dn.nsplit > 1 ? launch_stream_wide<kPartial, false>(p, stream_down_grid(E, H, I), stream)
+                                : launch_stream_wide<kScatter, false>(p, stream_down_grid(E, H, I), stream);
         } else {
             err = dn.nsplit > 1 ? launch_stream_epi<kPartial>(p, dn.d, stream_down_grid(E, H, I), stream)
                                 : launch_stream_epi<kScatter>(p, dn.d, stream_down_grid(E, H, I), stream);

@@ -518,16 +518,19 @@ def test_ffn_streaming_schedule_edges(ops, T, H, E, K, I, pattern):
 
 @pytest.mark.parametrize("T,H,E,K,I,pattern", [
     (256, 1024, 8, 2, 2048, "uniform"),  # 64 rows per expert: gate/up K in 2 chunks, down (one K-range) in 4
-    (200, 512, 8, 2, 2560, "skewed"),    # one expert 150 rows (passes of 128 + 22), down over 2 K-ranges (partials)
+    (200, 512, 8, 2, 2560, "skewed"),    # 50 rows per expert: 64-row passes; one expert 150 rows (64 + 64 + 22),
+                                         # down over 2 K-ranges (partials) staged in chunks of 256
+    (384, 2048, 16, 2, 1024, "uniform"), # 48 rows per expert: 64-row passes, gate/up K in 2 chunks of 1024
     (140, 256, 4, 2, 512, "invalid"),    # 70 rows per expert, single chunks, ids outside [0, E)
     (160, 640, 8, 2, 1024, "uniform"),   # H = 640 (a multiple of 128, not of 256): gate/up ring depth 4
     (2048, 256, 64, 2, 512, "uniform"),  # E = 64, 64 rows per expert: the id scans over 4096 slots per expert
-    (512, 256, 64, 6, 512, "zipf"),      # E = 64, K = 6, Zipf(1.1) experts: the head expert takes several passes
+    (512, 256, 64, 6, 512, "zipf"),      # E = 64, K = 6, Zipf(1.1) experts, 48 rows per expert on average (64-row
+                                         # passes): the head expert takes several passes
     (8192, 128, 256, 2, 256, "zipf"),    # E = 256, 64 rows per expert on average, head experts of thousands of rows
 ])
 def test_ffn_wide_streaming_schedule(ops, T, H, E, K, I, pattern):
     """32 to 72 rows per expert on average (80 when I >= 4096): the weight-streaming schedule with the wide kernels
-    (up to 128 rows per pass, the K-range staged in chunks). offsets / sorted_slot and expert_out against the oracle
+    (up to 128 rows per pass, or 64 below 52 rows per expert on average; the K-range staged in chunks). offsets / sorted_slot and expert_out against the oracle
     on every slot, so every expert's first and last sorted rows and every pass of the experts above 128 rows are
     checked."""
     assert ffn_schedule(T, H, E, K, I) == 0
