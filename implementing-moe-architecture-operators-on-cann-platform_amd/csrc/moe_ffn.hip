@@ -39,10 +39,14 @@ size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 //   H = 4096, E = 128, K = 8, I = 1536   1160 / 1241, 1264 / 1250  (~77)
 //   H = 5120, E = 16, K = 2, I = 1536     241 / 253,  270 / 264   (~74)
 //   H = 7168, E = 256, K = 8, I = 2048   5427 / 5297 at 64 rows, 5029 / 5259 at 56  (~61)
-// so the wide kernels run to 80 rows when I >= 4096 and to 72 below.
+// so the wide kernels run to 72 rows below I = 4096. From I = 4096 they run to 96 rows, measured again with the
+// wide kernels' short passes (moe_ffn_stream.hip), the FFN (wide / tiled, us, one box):
+//   H = 2048, E = 16, K = 2, I = 8192     80 rows 408.6 / 442.2, 88 rows 419.6 / 452.4, 96 rows 431.8 / 450.8,
+//                                         112 rows 612.5 / 468.1 (experts above 128 rows take a second pass)
+//   H = 4096, E = 8,  K = 2, I = 14336    80 rows 726.7 / 784.0, 96 rows 779.1 / 804.8, 112 rows 1143.3 / 822.5
 // Shapes the wide kernels cannot run switch to the tiled schedule at 32 rows.
 constexpr int64_t kTiledMinRowsPerExpert = 32;
-constexpr int64_t kWideMaxRowsPerExpert = 80;
+constexpr int64_t kWideMaxRowsPerExpert = 97;
 constexpr int64_t kWideMaxRowsSmallI = 72;
 constexpr int64_t kWideLargeI = 4096;
 

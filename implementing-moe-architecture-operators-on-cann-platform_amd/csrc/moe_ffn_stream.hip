@@ -54,6 +54,8 @@
 // LDS: row r of the staged K-range at r * (kc + 8) halfs (16 B of padding per row puts the 16 rows read by one
 // ds_read_b128 in different banks), then the eight 2 KB re-layout buffers.
 
+#include <cmath>
+
 #include "moe_device.h"
 #include "moe_launch.h"
 
@@ -1069,9 +1071,20 @@ bool stream_wide_low(int64_t T, int H, int64_t E, int64_t K, int I) {
            wide_chunk(dn.kc, kWideRows, kWideDepthLow) > 0;
 }
 
-// The wide kernels run from kWideMinRows rows per expert on average (the 32-row passes then start to repeat).
+// The 32-row kernels stream an expert's weights once per 32 rows, so a single expert above 32 rows doubles the time
+// of its units, and those end the launch. The wide kernels therefore run from the average m at which the expected
+// largest of E counts of a uniform routing, about m + sqrt(2 ln E * m), passes 32 rows (m ~ 22 at E = 8, 21 at 16,
+// 19 at 64, 18 at 256), and from kWideMinRows whatever E. The FFN (32-row / wide kernels, us, two boxes):
+//   H = 2048, E = 16, K = 2, I = 8192:   22 rows 267.9 / 293.3, 24 rows 270.7 / 289.9, 26 rows 406.3 / 298.5
+//   H = 2048, E = 64, K = 6, I = 1408:   18 rows 189.8 / 220.1, 19.5 rows 281.8 / 223.6, 24 rows 291.2 / 231.3
+//   H = 4096, E = 8,  K = 2, I = 14336:  24 rows 521.4 / 500.9, 28 rows 776.8 / 550.4
+//   H = 4096, E = 128, K = 8, I = 1536:  20 rows 1290.8 / 827.2
+//   H = 7168, E = 256, K = 8, I = 2048:  18 rows 4212.8 / 3637.5, 20 rows 6342.1 / 3714.7
+// Skewed routing reaches the second pass at lower averages still; below it the wide kernels cost up to ~10 % more.
 bool stream_wide(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
-    return T * K >= kWideMinRows * E && stream_wide_supported(static_cast<int>(H), static_cast<int>(I));
+    const double m = static_cast<double>(T * K) / static_cast<double>(E);
+    const bool past = T * K >= kWideMinRows * E || m + std::sqrt(2.0 * std::log(static_cast<double>(E)) * m) > kMaxRows;
+    return past && stream_wide_supported(static_cast<int>(H), static_cast<int>(I));
 }
 
 int stream_gateup_grid(int T, int H, int E, int K, int I, bool wide, bool gateup_split) {

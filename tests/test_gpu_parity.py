@@ -527,12 +527,14 @@ def test_ffn_streaming_schedule_edges(ops, T, H, E, K, I, pattern):
     (512, 256, 64, 6, 512, "zipf"),      # E = 64, K = 6, Zipf(1.1) experts, 48 rows per expert on average (64-row
                                          # passes): the head expert takes several passes
     (8192, 128, 256, 2, 256, "zipf"),    # E = 256, 64 rows per expert on average, head experts of thousands of rows
+    (240, 256, 64, 6, 512, "uniform"),   # 22.5 rows per expert: wide at E = 64 (from ~19), though below 32
+    (352, 512, 8, 2, 4096, "uniform"),   # 88 rows per expert, I >= 4096: still wide (to 96), experts above 128 rows
 ])
 def test_ffn_wide_streaming_schedule(ops, T, H, E, K, I, pattern):
-    """32 to 72 rows per expert on average (80 when I >= 4096): the weight-streaming schedule with the wide kernels
-    (up to 128 rows per pass, or 64 below 52 rows per expert on average; the K-range staged in chunks). offsets / sorted_slot and expert_out against the oracle
-    on every slot, so every expert's first and last sorted rows and every pass of the experts above 128 rows are
-    checked."""
+    """~18-22 to 72 rows per expert on average (96 when I >= 4096): the weight-streaming schedule with the wide kernels
+    (up to 128 rows per pass; up to 56 rows per expert on average an expert's last pass of at most 64 rows runs with
+    the deeper ring; the K-range staged in chunks). offsets / sorted_slot and expert_out against the oracle on every
+    slot, so every expert's first and last sorted rows and every pass of the experts above 128 rows are checked."""
     assert ffn_schedule(T, H, E, K, I) == 0
     rng = np.random.default_rng(T + E + I)
     x = rng.standard_normal((T, H)).astype(np.float16)
