@@ -1081,9 +1081,24 @@ bool stream_wide_low(int64_t T, int H, int64_t E, int64_t K, int I) {
 //   H = 4096, E = 128, K = 8, I = 1536:  20 rows 1290.8 / 827.2
 //   H = 7168, E = 256, K = 8, I = 2048:  18 rows 4212.8 / 3637.5, 20 rows 6342.1 / 3714.7
 // Skewed routing reaches the second pass at lower averages still; below it the wide kernels cost up to ~10 % more.
+// Where 32 rows of H do not fit the LDS (H above 2272) the 32-row gate/up splits H into K-ranges or runs 16-row
+// passes, and given enough units to fill the CUs the wide kernels (which stage H in chunks) are faster from fewer
+// rows: from 16 rows per expert where 16 rows of H fit (H up to 4568), from 4 where none do (32-row / wide, us):
+//   H = 7168, E = 256, K = 8, I = 2048:  4 rows 3520.5 / 3261.1, 8 rows 3791.1 / 3460.3, 16 rows 4101.7 / 3628.6
+//   H = 4096, E = 128, K = 8, I = 1536:  8 rows 740.7 / 750.5,  12 rows 843.5 / 782.3, 16 rows 855.9 / 797.1
+//   H = 4096, E = 8,   K = 2, I = 14336: 12 rows 486.4 / 501.1, 16 rows 499.7 / 486.6
+// With fewer units (H = 5120, E = 16, I = 1536: 192 units of 128 columns for 256 CUs) the 32-row kernels stay
+// ahead: 4 / 8 / 16 rows 119.5 / 136.3 / 146.5 against 132.1 / 143.3 / 156.9 us.
+constexpr int64_t kWideManyUnits = 512;
+int64_t wide_min_rows(int H, int64_t E, int I) {
+    const StreamShape whole = pick_shape(H, false);
+    if (E * ((I + 127) / 128) < kWideManyUnits || (whole.kc > 0 && whole.rows_cap == kMaxRows)) return kWideMinRows;
+    return whole.kc > 0 ? 16 : 4;
+}
 bool stream_wide(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
     const double m = static_cast<double>(T * K) / static_cast<double>(E);
-    const bool past = T * K >= kWideMinRows * E || m + std::sqrt(2.0 * std::log(static_cast<double>(E)) * m) > kMaxRows;
+    const bool past = T * K >= wide_min_rows(static_cast<int>(H), E, static_cast<int>(I)) * E ||
+                      m + std::sqrt(2.0 * std::log(static_cast<double>(E)) * m) > kMaxRows;
     return past && stream_wide_supported(static_cast<int>(H), static_cast<int>(I));
 }
 

@@ -851,12 +851,16 @@ def tiled_down_grid(cfg) -> int:
     return plan.down_grid
 
 
-def test_deepseek_v3_layer_shape_sampled(ops):
+@pytest.mark.parametrize("T", [
+    2048,  # 64 rows per expert on average: the wide streaming kernels
+    256,   # 8 rows: also the wide kernels (16 rows of H = 7168 do not fit the 32-row kernels' LDS)
+])
+def test_deepseek_v3_layer_shape_sampled(ops, T):
     """The DeepSeek-V3 layer's expert shape (H = 7168, E = 256, K = 8, I = 2048; 22.5 GB of fp16 expert
-    weights) through moe_layer on 2048 Zipf-routed tokens: routing on every token against the oracle, expert_out
+    weights) through moe_layer on T Zipf-routed tokens: routing on every token against the oracle, expert_out
     against the oracle on six tokens (the oracle gets only their experts' weights), y bit for bit the combine of
     expert_out, and the three operators' run bit for bit."""
-    cfg = synth.MoeConfig(2048, 7168, 256, 8, 2048, zipf=True, name="deepseek_v3_shape")
+    cfg = synth.MoeConfig(T, 7168, 256, 8, 2048, zipf=True, name="deepseek_v3_shape")
     log(f"[{cfg.name}] T={cfg.T} H={cfg.H} E={cfg.E} K={cfg.K} I={cfg.I}: generating inputs on the GPU")
     x_d, wg_d, ew_d = gpu_inputs(ops, cfg, 45)
     y_d, ids_d, w_d, eo_d = ops.moe_layer_fused(x_d, wg_d, ew_d, cfg.K)

@@ -97,17 +97,18 @@ def test_no_alloc_two_calls_second_smaller(ops):
 
 
 @pytest.mark.parametrize("T1,T2,H,E,K,I", [
-    (1100, 800, 4096, 128, 2, 2048),  # first call: 16-row streaming passes over the whole of H (17 rows per
-                                      # expert: from ~19 at E = 128 the wide kernels run, which do not split H)
-    (560, 200, 7168, 256, 8, 512),    # first call: the tiled schedule (7168 does not fit LDS unsplit; 17.5 rows
-                                      # per expert, below the wide kernels' ~18 at E = 256)
+    (960, 800, 4096, 128, 2, 2048),   # first call: 16-row streaming passes over the whole of H (15 rows per expert:
+                                      # the wide kernels, which do not split H, run from 16 here)
+    (127, 100, 7168, 256, 8, 2048),   # first call: the tiled schedule (7168 does not fit LDS unsplit; 3.97 rows per
+                                      # expert, below the wide kernels' 4 at this H)
 ])
 def test_no_alloc_long_hidden_split_only_where_it_fits(ops, T1, T2, H, E, K, I):
     """An H too long for the 32-row gate/up kernel's LDS: moe_expert_ffn splits it over K-ranges into fp32 partial
-    sums. On the first call those partials (~72 MB) exceed the fixed scratch, so the no-alloc call runs gate/up
-    unsplit (fp32 summation order differs: held to 1e-2 max abs against moe_expert_ffn and to the north_star
-    thresholds against the oracle on a token sample); the second, smaller call's partials fit, so it splits like
-    moe_expert_ffn and is bit-identical to it."""
+    sums. On the first call those partials and the rest of the workspace exceed the fixed 64 MiB scratch, so the
+    no-alloc call runs gate/up unsplit, or the tiled schedule where H cannot run unsplit (fp32 summation order
+    differs: held to 1e-2 max abs against moe_expert_ffn and to the north_star thresholds against the oracle on a
+    token sample); the second, smaller call's partials fit, so it splits like moe_expert_ffn and is bit-identical
+    to it."""
     x, ids_d, ew = inputs(ops, T1, H, E, K, I, 48)
     ids = ids_d.cpu().numpy()
     for T in (T1, T2):
