@@ -117,6 +117,7 @@ struct StreamArgs {
     int32_t* sorted_out;
     int32_t* slot_row_out;        // and the inverse: slot_row[slot] = sorted row, for the slots of valid ids
     uint16_t* expert_out;         // gate/up zeroes the rows of ids outside [0, E)
+    int deal_active;              // deal the units of the active experts only (T*K <= E: most experts have no rows)
 };
 
 __device__ __forceinline__ void lds_barrier() {
@@ -386,21 +387,124 @@ __device__ __forceinline__ void expert_rank(const StreamArgs& p, int e, int befo
     }
 }
 
+// ---- units over the active experts ----
+// The persistent grid deals out only the units of experts that have rows. Dealt over all E experts, the units of
+// the few experts a small batch touches fall to the few workgroups whose unit range holds them (at T = 1 and
+// E = 256, 8 of 256 CUs stream all the weights). A 256-bit mask in LDS (E <= 256) names the active experts: bit
+// e of s_am[e / 64]; it is read afresh where needed rather than held in registers across the unit loop.
+__device__ __forceinline__ uint64_t uniform64(uint64_t v) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// gate/up: every workgroup ORs the valid ids of all T*K slots into the mask (4 id loads in flight per thread,
+// then a wave OR and one 64-bit LDS OR per wave and word)
+__device__ __forceinline__ void active_from_ids(const StreamArgs& p, unsigned long long* s_am) {
+    const int tid = static_cast<int>(threadIdx.x), lane = lane_id();
+    if (tid < 4) s_am[tid] = 0;
+    lds_barrier();
+    uint64_t m[4] = {0, 0, 0, 0};
+    for (int base = 0; base < p.S; base += 4 * kThreads) {
+        int id[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int sl = base + t * kThreads + tid;
+            id[t] = sl < p.S ? p.ids[sl] : -1;
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const bool valid = id[t] >= 0 && id[t] < p.E;
+            const uint64_t bit = valid ? uint64_t{1} << (id[t] & 63) : 0;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) m[w] |= (id[t] >> 6) == w ? bit : 0;
+        }
+    }
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+#pragma unroll
+        for (int d = 1; d < kWave; d <<= 1) m[w] |= __shfl_xor(m[w], d, kWave);
+        if (lane == 0 && m[w] != 0) atomicOr(&s_am[w], static_cast<unsigned long long>(m[w]));
+    }
+    lds_barrier();
+}
+
+// the down projection: the experts whose offsets (written by gate/up) enclose rows
+__device__ __forceinline__ void active_from_offsets(const StreamArgs& p, unsigned long long* s_am) {
+    const int tid = static_cast<int>(threadIdx.x);
+    if (tid < 4 * kWave) {  // waves 0-3, one mask word each
+        const int e = tid;
+        const uint64_t m = __ballot(e < p.E && p.offsets[e + 1] > p.offsets[e]);
+        if (tid % kWave == 0) s_am[tid / kWave] = m;
+    }
+    lds_barrier();
+}
+
+__device__ __forceinline__ uint64_t am_word(const unsigned long long* s_am, int w) { return uniform64(s_am[w]); }
+
+__device__ __forceinline__ int active_count(const unsigned long long* s_am) {
+    return __popcll(am_word(s_am, 0)) + __popcll(am_word(s_am, 1)) + __popcll(am_word(s_am, 2)) +
+           __popcll(am_word(s_am, 3));
+}
+
+// the a-th active expert (a < active_count)
+__device__ __forceinline__ int nth_active(const unsigned long long* s_am, int a) {
+    for (int w = 0; w < 4; ++w) {
+        const int c = __popcll(am_word(s_am, w));
+        if (a < c) {
+            uint64_t m = am_word(s_am, w);
+            for (int i = 0; i < a; ++i) m &= m - 1;
+            return w * 64 + __builtin_ctzll(m);
+        }
+        a -= c;
+    }
+    return -1;
+}
+
+// the highest active expert below e (-1 if none) and the lowest above e (-1 if none)
+__device__ __forceinline__ int prev_active(const unsigned long long* s_am, int e) {
+    for (int w = e >> 6; w >= 0; --w) {
+        uint64_t m = am_word(s_am, w);
+        if (w == (e >> 6)) m &= (uint64_t{1} << (e & 63)) - 1;
+        if (m != 0) return w * 64 + 63 - __builtin_clzll(m);
+    }
+    return -1;
+}
+__device__ __forceinline__ int next_active(const unsigned long long* s_am, int e) {
+    for (int w = e >> 6; w < 4; ++w) {
+        uint64_t m = am_word(s_am, w);
+        if (w == (e >> 6)) m &= (e & 63) == 63 ? 0 : ~((uint64_t{2} << (e & 63)) - 1);
+        if (m != 0) return w * 64 + __builtin_ctzll(m);
+    }
+    return -1;
+}
+
+// gate/up, at an active expert e's first unit: offsets_out of e and of the experts without rows before it (all
+// equal to e's offset), and for the last active expert those after it up to E (off + ne)
+__device__ __forceinline__ void write_offsets(const StreamArgs& p, const unsigned long long* s_am, int e, int off,
+                                              int ne) {
+    const int tid = static_cast<int>(threadIdx.x);
+    for (int x = prev_active(s_am, e) + 1 + tid; x <= e; x += kThreads) p.offsets_out[x] = off;
+    if (next_active(s_am, e) < 0)
+        for (int x = e + 1 + tid; x <= p.E; x += kThreads) p.offsets_out[x] = off + ne;
+}
+
 // Persistent grid: workgroup b takes units [b * units_per_wg, (b + 1) * units_per_wg) of E * nsplit * groups
-// units, unit u -> (expert, K-range, column group) with the column group fastest.
-template <int D, int EPI>
+// units, unit u -> (expert, K-range, column group) with the column group fastest. With DEAL (T*K <= E, so most
+// experts have no rows) it takes units [b * per, (b + 1) * per) of the active experts' units instead, per =
+// ceil(active units / grid), active unit ua -> (a-th active expert, K-range, column group); the unit's index u among
+// all E experts' units still fixes its ring rotation, so the results do not depend on the deal.
+template <int D, int EPI, bool DEAL>
 __global__ __launch_bounds__(kThreads) void ffn_stream_kernel(StreamArgs p, int units_per_wg) {
     extern __shared__ __align__(16) uint16_t lds[];
     __shared__ int s_eq[kWaves], s_lt[kWaves];
     __shared__ int s_rows[kMaxRows];
+    __shared__ unsigned long long s_am[4];
     const int wave = static_cast<int>(threadIdx.x) / kWave;
     const int lane = lane_id();
     const int tid = static_cast<int>(threadIdx.x);
     const int cols_per_wave = gate_up(EPI) ? 16 : 32;  // gate/up: 16 rows of each matrix; down: 32 rows
     const int groups = (p.ndim + kWaves * cols_per_wave - 1) / (kWaves * cols_per_wave);
-    const int total_units = p.E * p.nsplit * groups;
-    const int u_begin = static_cast<int>(blockIdx.x) * units_per_wg;
-    const int u_end = min(u_begin + units_per_wg, total_units);
     const int row = lane & 15, kg = lane >> 4;
     const int nsteps = p.kc / 32;
     const int gpr = p.kc / 8;
@@ -427,12 +531,34 @@ __global__ __launch_bounds__(kThreads) void ffn_stream_kernel(StreamArgs p, int 
         }
     }
 
+    const int upe = groups * p.nsplit;  // units per expert
+    int ua_begin, ua_end;
+    if constexpr (DEAL) {
+        if (gate_up(EPI)) active_from_ids(p, s_am);
+        else active_from_offsets(p, s_am);
+        const int nact = active_count(s_am);
+        const int per = (nact * upe + static_cast<int>(gridDim.x) - 1) / static_cast<int>(gridDim.x);
+        ua_begin = min(nact * upe, static_cast<int>(blockIdx.x) * per);
+        ua_end = min(nact * upe, ua_begin + per);
+        if (gate_up(EPI) && nact == 0 && blockIdx.x == 0)  // no valid ids: every offset is 0
+            for (int x = tid; x <= p.E; x += kThreads) p.offsets_out[x] = 0;
+    } else {
+        ua_begin = static_cast<int>(blockIdx.x) * units_per_wg;
+        ua_end = min(ua_begin + units_per_wg, p.E * upe);
+    }
     int cur_e = -1, off = 0, ne = 0, before = 0;          // expert whose counts are known (gate/up)
     int staged_e = -1, staged_split = -1, staged_mc = -1;  // activation rows held in LDS
-    for (int u = u_begin; u < u_end; ++u) {
+    for (int ua = ua_begin; ua < ua_end; ++ua) {
+        int e, u;
+        if constexpr (DEAL) {
+            e = nth_active(s_am, ua / upe);
+            u = e * upe + ua % upe;
+        } else {
+            u = ua;
+            e = u / upe;
+        }
         const int g = u % groups;
         const int split = (u / groups) % p.nsplit;
-        const int e = u / groups / p.nsplit;
         if (gate_up(EPI)) {
             if (e != cur_e) {
                 if (cur_e >= 0) lds_barrier();  // every wave is done with the previous expert's counts and rows
@@ -449,9 +575,13 @@ __global__ __launch_bounds__(kThreads) void ffn_stream_kernel(StreamArgs p, int 
                 }
                 cur_e = e;
                 staged_mc = -1;
-                if (g == 0 && split == 0 && tid == 0) {
-                    p.offsets_out[e] = off;
-                    if (e == p.E - 1) p.offsets_out[p.E] = off + ne;
+                if (g == 0 && split == 0) {
+                    if constexpr (DEAL) {
+                        write_offsets(p, s_am, e, off, ne);
+                    } else if (tid == 0) {
+                        p.offsets_out[e] = off;
+                        if (e == p.E - 1) p.offsets_out[p.E] = off + ne;
+                    }
                 }
             }
         } else {
@@ -945,12 +1075,16 @@ hipError_t launch_stream_epi(const StreamArgs& p, int d, int units, hipStream_t 
     case DEPTH: {                                                                                              \
         if constexpr (DEPTH > kMaxDepth) return hipErrorInvalidValue;                                           \
         else {                                                                                                 \
-        const void* fn = reinterpret_cast<const void*>(&ffn_stream_kernel<DEPTH, EPI>);                        \
+        const void* fn = p.deal_active ? reinterpret_cast<const void*>(&ffn_stream_kernel<DEPTH, EPI, true>)    \
+                                       : reinterpret_cast<const void*>(&ffn_stream_kernel<DEPTH, EPI, false>);  \
         err = ensure_lds_limit(fn, kLdsMax);                                                                   \
         if (err != hipSuccess) return err;                                                                     \
         const int slots = resident_workgroups(fn, kThreads, lds);                                              \
         const int upw = slots > 0 ? (units + slots - 1) / slots : 1;                                          \
-        ffn_stream_kernel<DEPTH, EPI><<<(units + upw - 1) / upw, kThreads, lds, stream>>>(p, upw);             \
+        if (p.deal_active)                                                                                     \
+            ffn_stream_kernel<DEPTH, EPI, true><<<(units + upw - 1) / upw, kThreads, lds, stream>>>(p, upw);   \
+        else                                                                                                   \
+            ffn_stream_kernel<DEPTH, EPI, false><<<(units + upw - 1) / upw, kThreads, lds, stream>>>(p, upw);  \
         break;                                                                                                 \
         }                                                                                                      \
     }
@@ -995,15 +1129,15 @@ hipError_t launch_stream_wide(const StreamArgs& p, int units, hipStream_t stream
 }
 
 // The kernel instantiation launch_stream_epi runs for ring depth d (nullptr for none).
-template <int EPI>
+template <int EPI, bool DEAL>
 const void* stream_kernel_fn(int d) {
     switch (d) {
         case 8:
-            if constexpr (gate_up(EPI)) return reinterpret_cast<const void*>(&ffn_stream_kernel<8, EPI>);
+            if constexpr (gate_up(EPI)) return reinterpret_cast<const void*>(&ffn_stream_kernel<8, EPI, DEAL>);
             else return nullptr;
-        case 4: return reinterpret_cast<const void*>(&ffn_stream_kernel<4, EPI>);
-        case 2: return reinterpret_cast<const void*>(&ffn_stream_kernel<2, EPI>);
-        case 1: return reinterpret_cast<const void*>(&ffn_stream_kernel<1, EPI>);
+        case 4: return reinterpret_cast<const void*>(&ffn_stream_kernel<4, EPI, DEAL>);
+        case 2: return reinterpret_cast<const void*>(&ffn_stream_kernel<2, EPI, DEAL>);
+        case 1: return reinterpret_cast<const void*>(&ffn_stream_kernel<1, EPI, DEAL>);
         default: return nullptr;
     }
 }
@@ -1013,17 +1147,25 @@ const void* stream_kernel_fn(int d) {
 hipError_t prepare_ffn_stream(int H, int I) {
     // the 32-row gate/up kernel of either layout that the call's size may pick: whole H, or H split into K-ranges
     const StreamShape whole = pick_shape(H, false), split = gateup_split_shape(H), dn = pick_shape(I, true);
-    const void* gu_fns[2] = {whole.kc > 0 ? stream_kernel_fn<kSwiGLU>(whole.d) : nullptr,
-                             split.kc > 0 && whole.rows_cap != kMaxRows ? stream_kernel_fn<kGatePartial>(split.d)
-                                                                        : nullptr};
-    if (!gu_fns[0] && !gu_fns[1]) return hipErrorInvalidValue;
-    const void* fns[3] = {gu_fns[0], gu_fns[1],
-                          dn.nsplit > 1 ? stream_kernel_fn<kPartial>(dn.d) : stream_kernel_fn<kScatter>(dn.d)};
-    if (!fns[2]) return hipErrorInvalidValue;
-    for (const void* fn : fns) {
-        if (!fn) continue;
-        const hipError_t err = ensure_lds_limit(fn, kLdsMax);
-        if (err != hipSuccess) return err;
+    // each with units dealt over all experts or over the active ones
+    for (const bool deal : {false, true}) {
+        const void* gu_fns[2] = {
+            whole.kc > 0 ? (deal ? stream_kernel_fn<kSwiGLU, true>(whole.d) : stream_kernel_fn<kSwiGLU, false>(whole.d))
+                         : nullptr,
+            split.kc > 0 && whole.rows_cap != kMaxRows
+                ? (deal ? stream_kernel_fn<kGatePartial, true>(split.d) : stream_kernel_fn<kGatePartial, false>(split.d))
+                : nullptr};
+        if (!gu_fns[0] && !gu_fns[1]) return hipErrorInvalidValue;
+        const void* dn_fn = dn.nsplit > 1
+                                ? (deal ? stream_kernel_fn<kPartial, true>(dn.d) : stream_kernel_fn<kPartial, false>(dn.d))
+                                : (deal ? stream_kernel_fn<kScatter, true>(dn.d) : stream_kernel_fn<kScatter, false>(dn.d));
+        const void* fns[3] = {gu_fns[0], gu_fns[1], dn_fn};
+        if (!fns[2]) return hipErrorInvalidValue;
+        for (const void* fn : fns) {
+            if (!fn) continue;
+            const hipError_t err = ensure_lds_limit(fn, kLdsMax);
+            if (err != hipSuccess) return err;
+        }
     }
     if (stream_wide_supported(H, I)) {
         const void* wide_fns[4] = {
@@ -1118,6 +1260,7 @@ hipError_t launch_ffn_stream(const uint16_t* x, const int32_t* expert_ids, const
     p.sorted_slot = ws.sorted_slot;
     p.ids = expert_ids;
     p.S = T * K;
+    p.deal_active = T * K <= E;
     p.offsets_out = ws.offsets;
     p.sorted_out = ws.sorted_slot;
     p.slot_row_out = ws.slot_row;

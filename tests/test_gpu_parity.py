@@ -565,6 +565,49 @@ def test_ffn_wide_streaming_schedule(ops, T, H, E, K, I, pattern):
     within(m, max_abs=1e-2, mean_abs=1e-3, cos=0.9999)
 
 
+@pytest.mark.parametrize("T,H,E,K,I,pattern", [
+    (1, 512, 256, 8, 256, "uniform"),   # one token: 8 active experts of 256
+    (5, 1024, 64, 6, 512, "invalid"),   # 30 slots, ids outside [0, E) among them
+    (2, 256, 32, 8, 256, "middle"),     # experts 10..19 only: empty experts before and after the active ones
+    (3, 256, 64, 4, 384, "ends"),       # experts 0 and 63 active, one expert twice
+    (2, 512, 16, 4, 4096, "uniform"),   # down projection split over I (fp32 partials) on the active experts
+    (2, 256, 16, 4, 256, "none"),       # no valid id at all: every offset 0, expert_out all zero
+])
+def test_ffn_streaming_dealt_over_active_experts(ops, T, H, E, K, I, pattern):
+    """T*K <= E: the streaming kernels deal their units over the experts that have rows, so the few active
+    experts' weights stream on the whole grid. Checked on a workspace filled with garbage first: offsets (written
+    for the empty experts too) and sorted_slot against a stable sort, expert_out against the oracle on every valid
+    slot and zero on the others."""
+    assert T * K <= E and ffn_schedule(T, H, E, K, I) == 0
+    rng = np.random.default_rng(T * 1000 + E + I)
+    x = rng.standard_normal((T, H)).astype(np.float16)
+    ew = np.concatenate([rng.standard_normal((E, 2 * I, H)) / math.sqrt(H),
+                         rng.standard_normal((E, I, H)) / math.sqrt(I)], axis=1).astype(np.float16)
+    if pattern == "middle":
+        ids = np.stack([rng.permutation(10)[:K] + 10 for _ in range(T)]).astype(np.int32)
+    elif pattern == "ends":
+        ids = np.stack([rng.permutation(E)[:K] for _ in range(T)]).astype(np.int32)
+        ids[0, 0], ids[1, 0], ids[2, 1] = 0, E - 1, ids[1, 1]
+    elif pattern == "none":
+        ids = np.full((T, K), -1, np.int32)
+        ids[1, 2] = E
+    else:
+        ids = np.stack([rng.permutation(E)[:K] for _ in range(T)]).astype(np.int32)
+        if pattern == "invalid":
+            ids[0, 1], ids[2, 0], ids[4, 5] = -1, E, 999
+    w = np.full((T, K), 0.5, np.float16)
+    valid = (ids >= 0) & (ids < E)
+    log(f"[dealt] {pattern}: T={T} H={H} E={E} K={K} I={I}; {len(np.unique(ids[valid]))} active experts")
+    x_d, ids_d, w_d, ew_d = dev(x), dev(ids), dev(w), dev(ew)
+    ws = torch.full((ops.workspace_bytes(T, H, E, K, I),), 0xAB, dtype=torch.uint8, device="cuda")
+    eo = f32(host(ops.MoeExpertFFN(x_d, ids_d, w_d, ew_d, 0, ws)))
+    check_permute(host(ws), ids, E)
+    assert not eo[~valid].any()
+    if valid.any():
+        eo_o = oracle.expert_ffn(f32(x), np.where(valid, ids, 0), f32(ew), I)
+        within(oracle.compare(eo[valid], eo_o[valid]), max_abs=1e-2, mean_abs=1e-3, cos=0.9999)
+
+
 @pytest.mark.parametrize("T,H,E,K,I,pattern,nsplit", [
     (64, 4096, 8, 2, 256, "uniform", 2),   # 32-row kernel, H in two K-ranges of 2048 (16 rows per expert)
     (24, 4096, 8, 2, 256, "uniform", 1),   # 6 rows per expert: one 16-row pass over the whole H, no partial sums
