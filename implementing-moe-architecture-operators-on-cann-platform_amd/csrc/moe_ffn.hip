@@ -132,7 +132,7 @@ FfnGrid ffn_grid(int T, int H, int E, int K, int I) {
     } else {
         g.block_threads = stream_block_threads();
         g.gateup_blocks = stream_gateup_grid(T, H, E, K, I, stream_wide(T, H, E, K, I));
-        g.down_blocks = stream_down_grid(E, H, I);
+        g.down_blocks = stream_down_grid(T, H, E, K, I, stream_wide(T, H, E, K, I));
         g.rows_per_tile = stream_rows_per_pass();
     }
     return g;

@@ -1065,6 +1065,39 @@ StreamShape gateup_wide_shape(int H) {
     return wide_chunk(H, kWideRows, kWideDepth) > 0 ? StreamShape{H, kWideDepth, kWideRows, 1} : StreamShape{0, 0, 0, 0};
 }
 
+// ---- tiny batches: K-ranges that fill the grid ----
+// With T*K <= E the 32-row kernels deal their units over the active experts, at most T*K of them. Where even T*K
+// active experts would give fewer than kTinyUnits units, the K-range is halved until they do (down to 256
+// columns; fp32 partial sums, reduced as for a long H or I): a single token's layer otherwise streamed its
+// weights on 48-66 CUs at ~45 GB/s each. The FFN (unsplit / halving below 128 units / below 256 units, us):
+//   H = 2048, E = 16, K = 2, I = 8192:   T = 1 56.2 / 48.4 / 47.0,  T = 2 75.4 / 75.6 / 74.0
+//   H = 2048, E = 64, K = 6, I = 1408:   T = 1 43.8 / 34.9 / 37.0,  T = 2 50.4 / 47.1 / 54.6
+//   H = 4096, E = 8,  K = 2, I = 14336:  T = 1 120.7 / 121.1 / 124.8
+//   H = 7168, E = 256, K = 8, I = 2048:  T = 1 119.3 / 119.4 / 124.5
+// (from ~200 units the reduce launch and the shorter rings cost more than the extra CUs bring).
+constexpr int kTinyUnits = 128;
+StreamShape tiny_split(StreamShape s, int kdim, int64_t slots, int groups, int max_d) {
+    const int kc_max32 = (kLdsMax - kTbBytes) / (kMaxRows * 2) - 8;
+    while (s.kc > 0 && slots * groups * s.nsplit < kTinyUnits) {
+        const int kc = s.kc / 2;
+        if (kc < 256 || kc % 32 != 0 || kdim % kc != 0) break;
+        int d = max_d;
+        while (d > 1 && kc % (32 * d) != 0) d /= 2;
+        s = StreamShape{kc, d, kc <= kc_max32 ? kMaxRows : 16, kdim / kc};
+    }
+    return s;
+}
+// The K-range layouts of a call: gate/up (whole H, split H, or the wide kernels' chunked H) and down.
+StreamShape stream_gateup_shape(int64_t T, int H, int64_t E, int64_t K, int I, bool wide, bool gateup_split) {
+    if (wide) return gateup_wide_shape(H);
+    const StreamShape s = gateup_shape(T, H, E, K, gateup_split);
+    return gateup_split && T * K <= E ? tiny_split(s, H, T * K, (I + kWaves * 16 - 1) / (kWaves * 16), 8) : s;
+}
+StreamShape stream_down_shape(int64_t T, int H, int64_t E, int64_t K, int I, bool wide) {
+    const StreamShape s = pick_shape(I, true);
+    return !wide && T * K <= E ? tiny_split(s, I, T * K, (H + kWaves * 32 - 1) / (kWaves * 32), 4) : s;
+}
+
 template <int EPI>
 hipError_t launch_stream_epi(const StreamArgs& p, int d, int units, hipStream_t stream) {
     const size_t lds = static_cast<size_t>(p.rows_cap) * (p.kc + 8) * sizeof(uint16_t) + (d >= 2 ? kTbBytes : 0);
@@ -1147,6 +1180,14 @@ const void* stream_kernel_fn(int d) {
 hipError_t prepare_ffn_stream(int H, int I) {
     // the 32-row gate/up kernel of either layout that the call's size may pick: whole H, or H split into K-ranges
     const StreamShape whole = pick_shape(H, false), split = gateup_split_shape(H), dn = pick_shape(I, true);
+    // the partial-sum kernels at every ring depth, which the tiny batches' K-ranges (tiny_split) may pick
+    for (const int d : {8, 4, 2, 1}) {
+        for (const void* fn : {stream_kernel_fn<kGatePartial, true>(d), stream_kernel_fn<kPartial, true>(d)}) {
+            if (!fn) continue;
+            const hipError_t err = ensure_lds_limit(fn, kLdsMax);
+            if (err != hipSuccess) return err;
+        }
+    }
     // each with units dealt over all experts or over the active ones
     for (const bool deal : {false, true}) {
         const void* gu_fns[2] = {
@@ -1186,8 +1227,8 @@ int stream_rows_per_pass() { return kMaxRows; }
 // One fp32 buffer serves both splits in turn: gate/up's sums are reduced into hidden before the down projection
 // writes its own. The wide gate/up kernel never splits H.
 size_t stream_partial_bytes(int T, int H, int E, int K, int I, bool wide, bool gateup_split) {
-    const StreamShape gu = wide ? gateup_wide_shape(H) : gateup_shape(T, H, E, K, gateup_split);
-    const StreamShape dn = pick_shape(I, true);
+    const StreamShape gu = stream_gateup_shape(T, H, E, K, I, wide, gateup_split);
+    const StreamShape dn = stream_down_shape(T, H, E, K, I, wide);
     const size_t rows = static_cast<size_t>(T) * K;
     const size_t g = gu.nsplit > 1 ? static_cast<size_t>(gu.nsplit) * rows * 2 * I * sizeof(float) : 0;
     const size_t d = dn.nsplit > 1 ? static_cast<size_t>(dn.nsplit) * rows * H * sizeof(float) : 0;
@@ -1245,12 +1286,11 @@ bool stream_wide(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I) {
 }
 
 int stream_gateup_grid(int T, int H, int E, int K, int I, bool wide, bool gateup_split) {
-    return E * ((I + kWaves * 16 - 1) / (kWaves * 16)) *
-           (wide ? gateup_wide_shape(H) : gateup_shape(T, H, E, K, gateup_split)).nsplit;
+    return E * ((I + kWaves * 16 - 1) / (kWaves * 16)) * stream_gateup_shape(T, H, E, K, I, wide, gateup_split).nsplit;
 }
 
-int stream_down_grid(int E, int H, int I) {
-    return E * ((H + kWaves * 32 - 1) / (kWaves * 32)) * pick_shape(I, true).nsplit;
+int stream_down_grid(int T, int H, int E, int K, int I, bool wide) {
+    return E * ((H + kWaves * 32 - 1) / (kWaves * 32)) * stream_down_shape(T, H, E, K, I, wide).nsplit;
 }
 
 hipError_t launch_ffn_stream(const uint16_t* x, const int32_t* expert_ids, const uint16_t* expert_weights,
@@ -1277,7 +1317,7 @@ hipError_t launch_ffn_stream(const uint16_t* x, const int32_t* expert_ids, const
     // experts with more than ~32 rows on average take the wide kernels (up to 128 rows per pass)
     const bool wide = stream_wide(T, H, E, K, I);
     const bool low = wide && stream_wide_low(T, H, E, K, I);
-    const StreamShape gu = wide ? gateup_wide_shape(H) : gateup_shape(T, H, E, K, gateup_split);
+    const StreamShape gu = stream_gateup_shape(T, H, E, K, I, wide, gateup_split);
     p.act = x;
     p.out = ws.hidden;
     p.partial = ws.partial;
@@ -1289,7 +1329,7 @@ hipError_t launch_ffn_stream(const uint16_t* x, const int32_t* expert_ids, const
     p.w_off = 0;
     p.w1_off = static_cast<size_t>(I) * H;
     p.gather = 1;
-    const StreamShape dn = pick_shape(I, true);
+    const StreamShape dn = stream_down_shape(T, H, E, K, I, wide);
     hipError_t err;
     {
         TraceScope trace("moe_ffn_gateup_swiglu", stream);
@@ -1330,15 +1370,15 @@ hipError_t launch_ffn_stream(const uint16_t* x, const int32_t* expert_ids, const
         TraceScope trace("moe_ffn_down", stream);
         if (wide && low) {
             p.kchunk = wide_chunk(dn.kc, kWideRows, kWideDepthLow);
-            err = dn.nsplit > 1 ? launch_stream_wide<kPartial, true>(p, stream_down_grid(E, H, I), stream)
-                                : launch_stream_wide<kScatter, true>(p, stream_down_grid(E, H, I), stream);
+            err = dn.nsplit > 1 ? launch_stream_wide<kPartial, true>(p, stream_down_grid(T, H, E, K, I, wide), stream)
+                                : launch_stream_wide<kScatter, true>(p, stream_down_grid(T, H, E, K, I, wide), stream);
         } else if (wide) {
             p.kchunk = wide_chunk(dn.kc, kWideRows, kWideDepth);
-            err = dn.nsplit > 1 ? launch_stream_wide<kPartial, false>(p, stream_down_grid(E, H, I), stream)
-                                : launch_stream_wide<kScatter, false>(p, stream_down_grid(E, H, I), stream);
+            err = dn.nsplit > 1 ? launch_stream_wide<kPartial, false>(p, stream_down_grid(T, H, E, K, I, wide), stream)
+                                : launch_stream_wide<kScatter, false>(p, stream_down_grid(T, H, E, K, I, wide), stream);
         } else {
-            err = dn.nsplit > 1 ? launch_stream_epi<kPartial>(p, dn.d, stream_down_grid(E, H, I), stream)
-                                : launch_stream_epi<kScatter>(p, dn.d, stream_down_grid(E, H, I), stream);
+            err = dn.nsplit > 1 ? launch_stream_epi<kPartial>(p, dn.d, stream_down_grid(T, H, E, K, I, wide), stream)
+                                : launch_stream_epi<kScatter>(p, dn.d, stream_down_grid(T, H, E, K, I, wide), stream);
         }
     }
     if (err != hipSuccess) return err;

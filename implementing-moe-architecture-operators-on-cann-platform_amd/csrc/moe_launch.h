@@ -99,7 +99,7 @@ bool stream_wide(int64_t T, int64_t H, int64_t E, int64_t K, int64_t I);
 hipError_t prepare_ffn_stream(int H, int I);  // kernel attributes, before the first launch of a call
 size_t stream_partial_bytes(int T, int H, int E, int K, int I, bool wide, bool gateup_split);
 int stream_gateup_grid(int T, int H, int E, int K, int I, bool wide, bool gateup_split = true);
-int stream_down_grid(int E, int H, int I);
+int stream_down_grid(int T, int H, int E, int K, int I, bool wide);
 // with y non-null (and weights) the combine is produced too: by the split reduce when the down projection is
 // split over K, else by the combine kernel after the FFN
 hipError_t launch_ffn_stream(const uint16_t* x, const int32_t* expert_ids, const uint16_t* expert_weights,
