@@ -170,7 +170,11 @@ def test_layer_empty_and_single_token(ops):
     assert np.array_equal(host(y_d).view(np.uint16), y_o.view(np.uint16))
 
 
-@pytest.mark.parametrize("T,H,E,K,I,schedule", [(64, 256, 8, 2, 512, 0), (512, 256, 4, 2, 512, 1)])
+@pytest.mark.parametrize("T,H,E,K,I,schedule", [
+    (64, 256, 8, 2, 512, 0),
+    (512, 256, 4, 2, 512, 1),
+    (2, 512, 64, 6, 1024, 0),  # T*K <= E: units dealt over the active experts, gate/up and down K-ranges halved
+])
 def test_layer_graph_replay_matches_eager(ops, T, H, E, K, I, schedule):
     """The layer's three C-ABI calls captured in one HIP graph: each replay, after eager work that changes x and
     clears the graph's outputs, equals an eager run on the same x bit for bit (ids, weights, expert_out, y), and
@@ -226,7 +230,11 @@ def test_layer_graph_replay_matches_eager(ops, T, H, E, K, I, schedule):
     del g
 
 
-@pytest.mark.parametrize("T,H,E,K,I,schedule", [(64, 256, 8, 2, 512, 0), (1000, 128, 16, 2, 128, 1)])
+@pytest.mark.parametrize("T,H,E,K,I,schedule", [
+    (64, 256, 8, 2, 512, 0),
+    (1000, 128, 16, 2, 128, 1),
+    (2, 512, 64, 6, 1024, 0),  # T*K <= E: units dealt over the active experts, gate/up and down K-ranges halved
+])
 def test_fused_layer_graph_replay(ops, T, H, E, K, I, schedule):
     """moe_layer (routing with the slot-ranking tail, one scatter launch, the FFN, the combine) captured in a HIP
     graph: every replay, after eager work that changes x and clears the outputs and the workspace, equals an eager
