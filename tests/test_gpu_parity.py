@@ -580,6 +580,8 @@ def test_ffn_wide_streaming_schedule(ops, T, H, E, K, I, pattern):
     (3, 256, 64, 4, 384, "ends"),       # experts 0 and 63 active, one expert twice
     (2, 512, 16, 4, 4096, "uniform"),   # down projection split over I (fp32 partials) on the active experts
     (2, 256, 16, 4, 256, "none"),       # no valid id at all: every offset 0, expert_out all zero
+    (1, 4096, 8, 2, 1024, "uniform"),   # H = 4096: the 16-row whole-H gate/up halved to 8 K-ranges of 512
+    (1, 7168, 16, 4, 512, "uniform"),   # H = 7168: gate/up's 4 K-ranges of 1792 halved to 8 of 896 (ring of 4)
 ])
 def test_ffn_streaming_dealt_over_active_experts(ops, T, H, E, K, I, pattern):
     """T*K <= E: the streaming kernels deal their units over the experts that have rows, so the few active
