@@ -154,6 +154,35 @@ def test_plans(lib):
     assert cp.grid * cp.block * cp.elems_per_thread >= 128 * 2048 and cp.workspace_bytes == 0
 
 
+def test_streaming_plan_grids(lib):
+    """The weight-streaming schedule's launch grids as the plan reports them (units of 128 gate/up columns or 256
+    down columns, times the K-ranges of the layout): with T*K <= E the K-ranges are halved until T*K experts would
+    make 128 units, and the wide kernels (which never split H) take over from ~18-22 rows per expert, or from 4
+    where the 32-row gate/up must split H."""
+    from conftest import package
+
+    lib_mod = package()._lib
+    fp = lib_mod.FfnPlan()
+
+    def grids(T, H, E, K, I):
+        assert lib.moe_expert_ffn_plan(T, H, E, K, I, C.byref(fp)) == MOE_OK
+        assert fp.schedule == 0
+        return fp.gateup_grid, fp.down_grid
+
+    # T = 1 at H = 2048, E = 64, K = 6, I = 1408: 6 slots x 11 column groups = 66 units -> H in 2 K-ranges (132);
+    # down 6 x 8 = 48 -> I in 4 K-ranges of 352 (192)
+    assert grids(1, 2048, 64, 6, 1408) == (64 * 11 * 2, 64 * 8 * 4)
+    # T = 1 at H = 2048, E = 16, K = 2, I = 8192: gate/up 2 x 64 = 128 units, whole H; down 2 x 8 x 4 = 64 ->
+    # I in 8 K-ranges of 1024
+    assert grids(1, 2048, 16, 2, 8192) == (16 * 64, 16 * 8 * 8)
+    # T*K > E: the layouts of a decode batch (down over 4 K-ranges of 2048)
+    assert grids(128, 2048, 16, 2, 8192) == (16 * 64, 16 * 8 * 4)
+    # DeepSeek-V3's experts at 4 rows per expert: the wide kernels (whole H) instead of 4 K-ranges of 1792
+    assert grids(128, 7168, 256, 8, 2048) == (256 * 16, 256 * 28)
+    # ... and at 2 rows per expert the 32-row kernels, H in 4 K-ranges
+    assert grids(64, 7168, 256, 8, 2048)[0] == 256 * 16 * 4
+
+
 def test_ffn_plan_at_the_32bit_bounds(lib):
     """Many rows per expert pick the LDS-tiled schedule also past 2 GiB of SwiGLU intermediate (hidden is
     addressed per tile); past its real 32-bit bounds (2 GiB of gathered x rows) the shape is rejected, never
