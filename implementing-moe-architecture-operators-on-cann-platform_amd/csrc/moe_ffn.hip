@@ -177,6 +177,8 @@ size_t layer_workspace_bytes(int64_t T, int64_t H, int64_t E, int64_t K, int64_t
     // counts for the routing blocks of any routing kernel: at most one block per 16 tokens
     if (ffn_schedule(T, H, E, K, I) == 1)
         bytes += align_up(sizeof(int32_t) * static_cast<size_t>((T + 15) / 16) * counts_stride(static_cast<int>(E)), 256);
+    else  // the split routing's quarter sums (small batches, E > 64)
+        bytes += align_up(routing_split_workspace_bytes(static_cast<int>(T), static_cast<int>(E)), 256);
     return bytes;
 }
 
@@ -205,7 +207,12 @@ hipError_t launch_layer(const uint16_t* x, const uint16_t* w_gate, const uint16_
         case 0: {
             hipError_t err = prepare_ffn_stream(H, I);  // the FFN kernels' attributes before the first launch
             if (err != hipSuccess) return err;
-            err = launch_routing_topk(x, w_gate, ids, weights, T, H, E, K, stream);
+            if (routing_split_applies(T, H, E, routing_lds_weights(w_gate, H, E))) {
+                float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + ffn_workspace_bytes(T, H, E, K, I));
+                err = launch_routing_split(x, w_gate, ids, weights, T, H, E, K, part, stream);
+            } else {
+                err = launch_routing_topk(x, w_gate, ids, weights, T, H, E, K, stream);
+            }
             if (err != hipSuccess) return err;
             return launch_ffn_combine(x, ids, weights, expert_weights, expert_out, y, ws, T, H, E, K, I, stream);
         }

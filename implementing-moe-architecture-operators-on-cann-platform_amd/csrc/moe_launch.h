@@ -35,6 +35,12 @@ int resident_workgroups(const void* fn, int threads, size_t lds);
 int routing_expert_blocks(int E);
 // lw: w_gate's rows can reach LDS 16 bytes at a time (E % 8 == 0, 16-byte aligned w_gate): routing_lds_weights
 bool routing_lds_weights(const void* w_gate, int H, int E);
+// moe_layer's routing of a batch of at most 16 tokens with E > 64: the quarters kernel's work over 4 * E / 32
+// workgroups, the fp32 quarter sums in `part` (routing_split_workspace_bytes), the same ids and weights
+bool routing_split_applies(int T, int H, int E, bool lw);
+size_t routing_split_workspace_bytes(int T, int E);
+hipError_t launch_routing_split(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H,
+                                int E, int K, float* part, hipStream_t stream);
 int routing_tokens_per_block(int T, int H, int E, bool lw);
 int routing_block_threads(int T, int H, int E, bool lw);
 int routing_lds_bytes(int T, int H, int E, bool lw);

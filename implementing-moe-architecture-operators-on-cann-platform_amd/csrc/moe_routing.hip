@@ -644,7 +644,7 @@ __global__ __launch_bounds__(kWideWaves * kWave) void routing_wide_kernel(const 
 // ((q0 + q1) + q2) + q3. The rows kernel sums the quarters one after the other in each wave; the quarters kernel
 // gives each quarter to a wave of its own. Both make the same fp32 operations for a token, so its logits, ids and
 // weights do not depend on which of them ran.
-__device__ __forceinline__ int quarter_begin(int j, int nst) { return j * nst / 4; }
+__host__ __device__ __forceinline__ int quarter_begin(int j, int nst) { return j * nst / 4; }
 
 constexpr int kRowWaves = 4;
 constexpr int kRowTokens = 16 * kRowWaves;
@@ -924,6 +924,133 @@ __global__ __launch_bounds__(4 * kWave) void routing_quarters_kernel(const uint1
         constexpr int MAXIT = (16 * kRankTopK + 4 * kWave - 1) / (4 * kWave);
         rank_slots<4, MAXIT>(expert_ids, t0 * K, min(T, t0 + 16) * K, E, counts_stride(E), reinterpret_cast<int*>(lds),
                              counts + static_cast<size_t>(blockIdx.x) * counts_stride(E), rank);
+    }
+}
+
+// ---- split routing of one 16-token block (moe_layer, E > 64, T <= 16) ----
+// At T <= 16 the quarters kernel's one workgroup reads all of w_gate on one CU (3.7 MB at E = 256, H = 7168:
+// ~50 us). Here workgroup (j, g) runs quarter j of the quarters kernel's k-steps for the kSplitGB expert blocks
+// of group g only (one wave), and writes its fp32 sums to the layer's workspace; a second launch adds the
+// quarters as the quarters kernel does, ((q0 + q1) + q2) + q3, and selects. Every expert's sum runs the same
+// MFMAs on the same fragments in the same k order, so ids and weights are the quarters kernel's bit for bit; only
+// the staging differs (a window of 16 kSplitGB experts, stages of kSplitSK k-steps).
+constexpr int kSplitGB = 2;
+constexpr int kSplitSK = row_stage_ksteps(kSplitGB);  // 8 k-steps of 32 rows x 32 experts: 16 KB per stage
+constexpr size_t kSplitLds = 2 * (16384 + size_t(kSplitSK) * 1024);
+
+template <int EB>
+__global__ __launch_bounds__(kWave) void routing_split_partial_kernel(const uint16_t* __restrict__ x,
+                                                                      const uint16_t* __restrict__ w_gate, int T,
+                                                                      int H, int E, float* __restrict__ part) {
+    constexpr int GB = kSplitGB, SK = kSplitSK;
+    constexpr int Gpad = GB * 16;
+    constexpr int kStage = SK * 32 * Gpad * 2;
+    static_assert(kStage == 16384 && EB % GB == 0, "stage geometry");
+    extern __shared__ __align__(16) uint8_t lds[];
+    uint8_t* wbuf = lds;               // [2][kStage]
+    uint8_t* xbuf = lds + 2 * kStage;  // [2][SK][16 rows][64 B]
+    const int lane = lane_id();
+    const int j = static_cast<int>(blockIdx.x) % 4, grp = static_cast<int>(blockIdx.x) / 4;
+    const int e0 = grp * Gpad;  // first expert of the window
+    // quarter j of the quarters kernel's k-steps (its stages hold row_stage_ksteps(EB) k-steps each); the host
+    // runs this kernel only where SK divides every quarter
+    constexpr int SKq = row_stage_ksteps(EB);
+    const int nstq = H / 32 / SKq;
+    const int k0 = SKq * quarter_begin(j, nstq);
+    const int n = (SKq * quarter_begin(j + 1, nstq) - k0) / SK;
+    const __amdgpu_buffer_rsrc_t wrs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(w_gate), 0, H * E * 2, 0x00020000);
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(x), 0, T * H * 2, 0x00020000);
+    const int xoff = (min(lane / 4, T - 1) * H + (lane % 4) * 8) * 2;
+    // w_gate copy: the quarters kernel's stage layout for GB blocks, columns e0 .. e0 + Gpad - 1 of each row
+    int woff[16];
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+        const int off = m * 1024 + lane * 16;
+        const int R = off / (32 * GB), pc = (off % (32 * GB)) / 16;
+        const int c = pc ^ ((R % 32) & (2 * GB - 1));
+        const int col = e0 + c * 8;
+        woff[m] = (R * E + (col < E ? col : 0)) * 2;  // padding chunks copy any valid chunk
+    }
+    const int arow = lane & 15, kg = lane >> 4;
+    int frag_off[2][GB];
+    {
+        const int sl = lane & 15;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int b = 0; b < GB; ++b) {
+                const int r = 8 * kg + 4 * h + sl / 4;
+                const int e = 16 * b + 4 * (sl % 4);
+                frag_off[h][b] = wstage_chunk<GB>(r, e / 8) + (e % 8) * 2;
+            }
+    }
+    auto issue = [&](int l) __attribute__((always_inline)) {
+        uint8_t* dst = wbuf + (l & 1) * kStage;
+#pragma unroll
+        for (int m = 0; m < 16; ++m)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (__attribute__((address_space(3))) void*)(dst + m * 1024), 16,
+                                                     static_cast<int>(woff[m]), (k0 + l * SK) * 32 * E * 2, 0, 0);
+#pragma unroll
+        for (int ks = 0; ks < SK; ++ks)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (__attribute__((address_space(3))) void*)(xbuf + ((l & 1) * SK + ks) * 1024),
+                                                     16, xoff, (k0 + l * SK + ks) * 64, 0, 0);
+    };
+    f32x4 acc[GB];
+#pragma unroll
+    for (int b = 0; b < GB; ++b) acc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (n > 0) issue(0);
+    for (int l = 0; l < n; ++l) {
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // this wave's copies of stage l (the only ones in flight)
+        const uint8_t* ws = wbuf + (l & 1) * kStage;
+        const uint8_t* xs = xbuf + (l & 1) * SK * 1024;
+        f16x8 a[SK], bv[SK][GB];
+#pragma unroll
+        for (int ks = 0; ks < SK; ++ks) {
+            a[ks] = *reinterpret_cast<const f16x8*>(xs + ks * 1024 + arow * 64 + kg * 16);
+            const uint8_t* wk = ws + ks * 32 * Gpad * 2;
+#pragma unroll
+            for (int b = 0; b < GB; ++b) {
+                const s16x4 lo = lds_read_tr16(wk + frag_off[0][b]);
+                const s16x4 hi = lds_read_tr16(wk + frag_off[1][b]);
+                bv[ks][b] = __builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+            }
+        }
+        if (l + 1 < n) issue(l + 1);  // refills the buffers of stage l - 1
+#pragma unroll
+        for (int ks = 0; ks < SK; ++ks)
+#pragma unroll
+            for (int b = 0; b < GB; ++b) acc[b] = mfma16x16x32(a[ks], bv[ks][b], acc[b]);
+    }
+#pragma unroll
+    for (int b = 0; b < GB; ++b)
+        *reinterpret_cast<f32x4*>(part + ((static_cast<size_t>(j) * EB + grp * GB + b) * kWave + lane) * 4) = acc[b];
+}
+
+// the quarters' sums in the quarters kernel's order, then its selection
+template <int EB>
+__global__ __launch_bounds__(kWave) void routing_split_select_kernel(const float* __restrict__ part,
+                                                                     int32_t* __restrict__ expert_ids,
+                                                                     uint16_t* __restrict__ weights, int T, int E,
+                                                                     int K) {
+    const int lane = lane_id(), kg = lane >> 4;
+    f32x4 acc[EB];
+#pragma unroll
+    for (int b = 0; b < EB; ++b) acc[b] = *reinterpret_cast<const f32x4*>(part + (static_cast<size_t>(b) * kWave + lane) * 4);
+#pragma unroll
+    for (int j = 1; j < 4; ++j)
+#pragma unroll
+        for (int b = 0; b < EB; ++b)
+            acc[b] = acc[b] + *reinterpret_cast<const f32x4*>(part + ((static_cast<size_t>(j) * EB + b) * kWave + lane) * 4);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        float v[EB];
+#pragma unroll
+        for (int b = 0; b < EB; ++b) v[b] = acc[b][r];
+        const int t = 4 * kg + r;
+        const bool active = t < T;
+        const int tr = active ? t : 0;
+        select_vals<EB>(v, E, K, active, expert_ids + static_cast<size_t>(tr) * K, weights + static_cast<size_t>(tr) * K);
     }
 }
 
@@ -1311,7 +1438,37 @@ RoutingKernel routing_kernel(int T, int H, int E, bool lw) {
     return T <= kQuartersMaxTokens ? kQuartersKernel : kRowsKernel;
 }
 
+template <int EB>
+hipError_t launch_split(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H, int E,
+                        int K, float* part, hipStream_t stream) {
+    const hipError_t attr = ensure_lds_limit(reinterpret_cast<const void*>(&routing_split_partial_kernel<EB>),
+                                             static_cast<int>(kSplitLds));
+    if (attr != hipSuccess) return attr;
+    TraceScope trace("moe_routing_topk", stream);
+    routing_split_partial_kernel<EB><<<4 * (EB / kSplitGB), kWave, kSplitLds, stream>>>(x, w_gate, T, H, E, part);
+    routing_split_select_kernel<EB><<<1, kWave, 0, stream>>>(part, ids, w, T, E, K);
+    return hipGetLastError();
+}
+
 }  // namespace
+
+bool routing_split_applies(int T, int H, int E, bool lw) {
+    if (T < 1 || T > 16 || routing_kernel(T, H, E, lw) != kQuartersKernel) return false;
+    const int skq = row_stage_ksteps(routing_expert_blocks(E)), nst = H / 32 / skq;
+    for (int j = 0; j < 4; ++j)
+        if (skq * (quarter_begin(j + 1, nst) - quarter_begin(j, nst)) % kSplitSK != 0) return false;
+    return true;
+}
+
+size_t routing_split_workspace_bytes(int T, int E) {
+    return T <= 16 && E > 64 ? static_cast<size_t>(4) * 16 * kWave * 16 : 0;  // [4 quarters][16 blocks][64 lanes] f32x4
+}
+
+hipError_t launch_routing_split(const uint16_t* x, const uint16_t* w_gate, int32_t* ids, uint16_t* w, int T, int H,
+                                int E, int K, float* part, hipStream_t stream) {
+    return routing_expert_blocks(E) == 8 ? launch_split<8>(x, w_gate, ids, w, T, H, E, K, part, stream)
+                                         : launch_split<16>(x, w_gate, ids, w, T, H, E, K, part, stream);
+}
 
 int routing_expert_blocks(int E) {
     const int eb = (E + 15) / 16;

@@ -1277,6 +1277,9 @@ def test_concurrent_threads_and_streams(ops):
     (9000, 256, 128, 4, 128, 1),   # E = 128, T > 8192: the rows kernel ranks its 64-token blocks
     (32790, 1024, 64, 6, 128, 1),  # 32 < E <= 64, T >= 32768: the resident kernel ranks each workgroup's run of
                                    # 9 token blocks (144 tokens, 864 slots) in one pass
+    (4, 2048, 256, 8, 128, 0),     # T <= 16, E > 64: split routing (32 workgroups of quarter sums, a selection)
+    (16, 1024, 128, 8, 256, 0),    # E = 128: 16 workgroups of quarter sums
+    (3, 1536, 160, 6, 128, 0),     # quarters of 12 k-steps (not a multiple of 8): the quarters kernel routes
 ])
 def test_fused_layer_matches_oracle_and_operators(ops, T, H, E, K, I, schedule):
     """moe_layer (routing that also ranks its blocks' slots, one scatter launch, the FFN, the combine): ids and
