@@ -207,7 +207,7 @@ moe_status moe_expert_ffn_no_alloc(const uint16_t* x, const int32_t* expert_ids,
  * moe_expert_ffn writes it, and y is bit-identical to moe_combine(expert_out, expert_ids, weights, y, ...).
  * When the weight-streaming schedule splits the down projection over K, the split reduce produces y as well,
  * saving the combine pass over expert_out; otherwise the combine kernel runs after the FFN. Deterministic (no
- * atomics). Workspace as for moe_expert_ffn. Sizes and errors as moe_expert_ffn plus moe_combine's checks.
+ * global atomics). Workspace as for moe_expert_ffn. Sizes and errors as moe_expert_ffn plus moe_combine's checks.
  * ---------------------------------------------------------------------------------------------------- */
 moe_status moe_expert_ffn_combine(const uint16_t* x, const int32_t* expert_ids, const uint16_t* weights,
                                   const uint16_t* expert_weights, uint16_t* expert_out, uint16_t* y,
@@ -220,8 +220,9 @@ moe_status moe_expert_ffn_combine(const uint16_t* x, const int32_t* expert_ids, 
  * routing, FFN, combine on one stream); the three operators stay the contract. On the LDS-tiled schedule the
  * routing kernel also ranks each token block's (token, k) slots by expert, so the FFN's permute is a single
  * scatter launch after it (the per-expert id scan of op_kernel/moe_expert_ffn.cpp:182-195, done once); on the
- * weight-streaming schedule it is routing followed by moe_expert_ffn_combine. expert_ids, weights, expert_out
- * and y are bit-identical to the three calls'. Deterministic (no atomics).
+ * weight-streaming schedule it is routing (for T <= 16 and E > 64 spread over 4 * E / 32 workgroups, whose fp32
+ * sums pass through the workspace) followed by moe_expert_ffn_combine. expert_ids, weights, expert_out and y are
+ * bit-identical to the three calls'. Deterministic (no global atomics; nothing depends on timing).
  * The workspace is moe_layer_workspace_bytes() (>= moe_expert_ffn_workspace_bytes()); 0 = unsupported sizes.
  * Sizes and errors as the three operators' checks together.
  * ---------------------------------------------------------------------------------------------------- */
